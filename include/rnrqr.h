@@ -1,0 +1,103 @@
+/*
+ * rnrqr.h -- C ABI of the MI355X (gfx950) reflector-free batched QR library, librnrqr.so.
+ *
+ * The library factors a batch of square fp32 matrices A (row-major, A[b][i][j] at
+ * A + b*batch_stride + i*n + j) into the compact LAPACK / torch.geqrf layout (H, tau)
+ * without forming or applying a Householder reflector:
+ *
+ *   I.   frame:   A = P L U (partial pivoting), then CholeskyQR2 on the unit-lower L,
+ *                 Q = P * (L Ra^-1 Rb^-1), each Cholesky on G + 1e-7*mean(diag G)*I;
+ *   II.  closure: R = triu(Q^T A);
+ *   III. chart:   sign-ruled unpivoted LU of I - Q S; its multipliers are the
+ *                 reflector tails Y, tau_k = 2 / (1 + ||Y[k+1:,k]||^2),
+ *                 H = triu(diag(s) R) + tril(Y, -1).
+ *
+ * Every entry point is asynchronous on the caller's HIP stream, never throws, keeps no
+ * global mutable state, and returns an rnr_status code.  Device pointers only.  The
+ * input is never written.  Calls that share one workspace must be ordered on one stream.
+ *
+ * Reference interfaces replaced (paths relative to the johnzfitch/qr-contest tree):
+ *   rnr_qr_f32      custom_kernel(data) -> (H, tau)      reflection_no_reflectors.py:181-196
+ *   rnr_frame_f32   _frame(A) -> Q                       reflection_no_reflectors.py:55-81
+ *   rnr_lu_f32      torch.linalg.lu(A) (P, L; U dropped) reflection_no_reflectors.py:66
+ *   rnr_cholqr_f32  _cholqr(M) -> M R^-1                 reflection_no_reflectors.py:68-77
+ *   rnr_chart_f32   _chart(Q) -> (Y, s), tau recompute   reflection_no_reflectors.py:86-176,192
+ */
+#ifndef RNRQR_H
+#define RNRQR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* rnr_stream_t; /* hipStream_t; NULL = the legacy default stream */
+
+enum rnr_status {
+  RNR_OK = 0,
+  RNR_ERR_INVALID_ARG = 1,    /* null pointer, negative size, stride < n*n */
+  RNR_ERR_UNSUPPORTED_N = 2,  /* n outside [1, RNR_MAX_N] */
+  RNR_ERR_WORKSPACE = 3,      /* workspace pointer null or smaller than the query result */
+  RNR_ERR_HIP = 4,            /* a HIP launch or attribute call failed */
+  RNR_ERR_MISALIGNED = 5      /* a pointer is not 4-byte aligned (workspace: 256-byte) */
+};
+
+#define RNR_MAX_N 2048
+
+/* Human-readable text of a status code (static storage, never NULL). */
+const char* rnr_status_string(int status);
+
+/* Library version, "major.minor.patch". */
+const char* rnr_version(void);
+
+/* ---- whole path: custom_kernel (reflection_no_reflectors.py:181-196) ------------------
+ * Bytes of device workspace rnr_qr_f32 needs for (batch, n).  0 for batch == 0. */
+int rnr_qr_f32_workspace(int64_t batch, int64_t n, size_t* bytes);
+
+/* H (batch x n x n, contiguous) and tau (batch x n, contiguous) from A.
+ * batch_stride is the element distance between consecutive input matrices (>= n*n).
+ * info (optional, batch ints, may be NULL): 0 on success; k > 0 when a Cholesky of
+ * matrix b met a non-positive or non-finite pivot at column k (the reference raises
+ * from torch.linalg.cholesky in that case, reflection_no_reflectors.py:76).
+ * ws: device workspace of at least rnr_qr_f32_workspace bytes, 256-byte aligned. */
+int rnr_qr_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride,
+               float* H, float* tau, int32_t* info,
+               void* ws, size_t ws_bytes, rnr_stream_t stream);
+
+/* ---- stage entry points (the reference's internal stages, for stage-level parity) ---- */
+
+/* Partial-pivot LU (torch.linalg.lu, reflection_no_reflectors.py:66): perm[b][i] is the
+ * row of A that lands in position i (A[perm] = L U, first-maximum pivot rule) and L
+ * (batch x n x n) is unit lower-triangular with exact zeros above the diagonal.  U is
+ * not returned: the reference discards it. */
+int rnr_lu_f32_workspace(int64_t batch, int64_t n, size_t* bytes);
+int rnr_lu_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride,
+               float* L, int32_t* perm, void* ws, size_t ws_bytes, rnr_stream_t stream);
+
+/* One CholeskyQR pass (_cholqr, reflection_no_reflectors.py:68-77): G = M^T M,
+ * G += 1e-7*mean(diag G)*I, R = chol(G) upper, Q = M R^-1.  R (optional, may be NULL)
+ * receives R in its upper triangle (the strict lower triangle is left unspecified). */
+int rnr_cholqr_f32_workspace(int64_t batch, int64_t n, size_t* bytes);
+int rnr_cholqr_f32(const float* M, int64_t batch, int64_t n, int64_t batch_stride,
+                   float* Q, float* R, int32_t* info,
+                   void* ws, size_t ws_bytes, rnr_stream_t stream);
+
+/* The orthogonal frame (_frame, reflection_no_reflectors.py:55-81): Q = P CholQR2(L). */
+int rnr_frame_f32_workspace(int64_t batch, int64_t n, size_t* bytes);
+int rnr_frame_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride,
+                  float* Q, int32_t* info, void* ws, size_t ws_bytes, rnr_stream_t stream);
+
+/* The chart (_chart, reflection_no_reflectors.py:86-176, and the tau recompute at :192),
+ * in place: on entry Y holds Q (batch x n x n, contiguous); on return its strict lower
+ * triangle holds the reflector tails (the upper triangle is left unspecified), s the
+ * signs (+1/-1) and tau = 2 / (1 + sum_{i>k} Y[i][k]^2).  No workspace. */
+int rnr_chart_f32(float* Y, int64_t batch, int64_t n, float* s, float* tau,
+                  rnr_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RNRQR_H */

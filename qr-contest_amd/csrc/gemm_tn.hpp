@@ -1,0 +1,153 @@
+// Batched "transpose-A" fp32 MFMA product restricted to upper-triangular tiles:
+//
+//   C[b][i][j] = rs[b][i] * sum_{r = klo}^{n-1} X[b][r][i] * Y[b][r][j]     (tile ti <= tj)
+//
+// It serves the three contractions of the path whose outputs are (block-)upper:
+//   * Gram of the unit-lower L, G = L^T L (klo = first column of the tile: the rows above
+//     it are exact zeros of L)        -- reflection_no_reflectors.py:73 (first pass)
+//   * Gram of Q1, G = Q1^T Q1         -- reflection_no_reflectors.py:73 (second pass)
+//   * closure, H_upper = diag(s) triu(Q^T A), written only on and above the diagonal so
+//     the reflector tails below it survive -- reflection_no_reflectors.py:186,195
+//
+// Tile BM x BM per 256-thread workgroup (2 x 2 waves, each BM/2 x BM/2 from 32x32 MFMA
+// blocks); the K dimension (rows of X and Y) is staged through double-buffered LDS in
+// chunks of 32 rows, so every operand element is read from HBM/L2 once per tile.
+#pragma once
+#include "common.hpp"
+
+namespace rnr {
+
+struct TnArgs {
+  const float* X;
+  int64_t sx;
+  const float* Y;
+  int64_t sy;
+  float* C;
+  int64_t sc;
+  const float* rs;  // row scale, batch stride n (ROW_SCALE only)
+  int n;
+  int nt;       // tiles per matrix edge
+  int ntiles;   // upper tiles per matrix
+  int total;    // grid size
+  int klo_from_j;
+};
+
+template <int BM, bool MASK_LOWER, bool ROW_SCALE, bool VEC4>
+__global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
+  constexpr int BK = 32;
+  constexpr int WM = BM / 2;
+  constexpr int NB = WM / 32;
+  constexpr int PER = BK * BM / 256;  // elements per thread per operand per chunk
+  __shared__ __attribute__((aligned(16))) float Xs[2][BK][BM];
+  __shared__ __attribute__((aligned(16))) float Ys[2][BK][BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int pid = xcd_remap(blockIdx.x, a.total);
+  const int b = pid / a.ntiles;
+  int ti, tj;
+  upper_tile(pid - b * a.ntiles, a.nt, ti, tj);
+  const int n = a.n, i0 = ti * BM, j0 = tj * BM;
+  const float* X = a.X + b * a.sx;
+  const float* Y = a.Y + b * a.sy;
+  const int wi0 = (wid >> 1) * WM, wj0 = (wid & 1) * WM;
+
+  f32x16 acc[NB][NB];
+#pragma unroll
+  for (int mi = 0; mi < NB; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < NB; ++nj) acc[mi][nj] = zero16();
+
+  float rx[PER], ry[PER];
+  auto gload = [&](int k) {
+    if constexpr (VEC4) {
+#pragma unroll
+      for (int p = 0; p < PER / 4; ++p) {
+        const int idx = tid + 256 * p;
+        const int row = idx / (BM / 4), c = 4 * (idx % (BM / 4));
+        const int gr = k + row;
+        float4 vx = make_float4(0.f, 0.f, 0.f, 0.f), vy = vx;
+        if (gr < n) {
+          if (i0 + c < n) vx = *reinterpret_cast<const float4*>(X + (int64_t)gr * n + i0 + c);
+          if (j0 + c < n) vy = *reinterpret_cast<const float4*>(Y + (int64_t)gr * n + j0 + c);
+        }
+        rx[4 * p + 0] = vx.x; rx[4 * p + 1] = vx.y; rx[4 * p + 2] = vx.z; rx[4 * p + 3] = vx.w;
+        ry[4 * p + 0] = vy.x; ry[4 * p + 1] = vy.y; ry[4 * p + 2] = vy.z; ry[4 * p + 3] = vy.w;
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < PER; ++p) {
+        const int idx = tid + 256 * p;
+        const int row = idx / BM, c = idx % BM;
+        const int gr = k + row;
+        rx[p] = (gr < n && i0 + c < n) ? X[(int64_t)gr * n + i0 + c] : 0.f;
+        ry[p] = (gr < n && j0 + c < n) ? Y[(int64_t)gr * n + j0 + c] : 0.f;
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+    if constexpr (VEC4) {
+#pragma unroll
+      for (int p = 0; p < PER / 4; ++p) {
+        const int idx = tid + 256 * p;
+        const int row = idx / (BM / 4), c = 4 * (idx % (BM / 4));
+        *reinterpret_cast<float4*>(&Xs[buf][row][c]) =
+            make_float4(rx[4 * p], rx[4 * p + 1], rx[4 * p + 2], rx[4 * p + 3]);
+        *reinterpret_cast<float4*>(&Ys[buf][row][c]) =
+            make_float4(ry[4 * p], ry[4 * p + 1], ry[4 * p + 2], ry[4 * p + 3]);
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < PER; ++p) {
+        const int idx = tid + 256 * p;
+        Xs[buf][idx / BM][idx % BM] = rx[p];
+        Ys[buf][idx / BM][idx % BM] = ry[p];
+      }
+    }
+  };
+
+  const int klo = a.klo_from_j ? j0 : 0;
+  int buf = 0;
+  gload(klo);
+  lstore(0);
+  __syncthreads();
+  for (int kc = klo; kc < n; kc += BK) {
+    const bool more = kc + BK < n;
+    if (more) gload(kc + BK);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 2) {
+      const int k = kk + h;
+      float av[NB], bv[NB];
+#pragma unroll
+      for (int mi = 0; mi < NB; ++mi) av[mi] = Xs[buf][k][wi0 + mi * 32 + l32];
+#pragma unroll
+      for (int nj = 0; nj < NB; ++nj) bv[nj] = Ys[buf][k][wj0 + nj * 32 + l32];
+#pragma unroll
+      for (int mi = 0; mi < NB; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < NB; ++nj) acc[mi][nj] = mfma(av[mi], bv[nj], acc[mi][nj]);
+    }
+    if (more) lstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  float* C = a.C + b * a.sc;
+  const float* rs = ROW_SCALE ? a.rs + (int64_t)b * n : nullptr;
+#pragma unroll
+  for (int mi = 0; mi < NB; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < NB; ++nj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = i0 + wi0 + mi * 32 + acc_row(r, lane);
+        const int col = j0 + wj0 + nj * 32 + l32;
+        if (row < n && col < n && (!MASK_LOWER || col >= row)) {
+          float v = acc[mi][nj][r];
+          if (ROW_SCALE) v *= rs[row];
+          C[(int64_t)row * n + col] = v;
+        }
+      }
+}
+
+}  // namespace rnr

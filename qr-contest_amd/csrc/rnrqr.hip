@@ -1,0 +1,315 @@
+// librnrqr: C ABI and launch sequence of the reflector-free batched QR for gfx950.
+//
+// Launch sequence of rnr_qr_f32 on the caller's stream (reflection_no_reflectors.py:181-196):
+//   1. k_lu<true>        A -> W (in-place factor, A's row order), perm, L      (:66)
+//   2. k_tn_upper        G = L^T L, upper tiles, zero rows of L skipped         (:73)
+//   3. k_chol            G -> R_a (upper, jittered), Dinv, info                 (:74-76)
+//   4. k_trsm            Q1 = L R_a^-1 -> W                                     (:77)
+//   5. k_tn_upper        G = Q1^T Q1                                            (:73)
+//   6. k_chol            G -> R_b, Dinv, info                                   (:74-76)
+//   7. k_trsm            Q = P (Q1 R_b^-1) -> Qb and H (row scatter)            (:77,81)
+//   8. k_lu<false>       chart in place on H: tails Y, signs s, tau             (:139-174,192)
+//   9. k_tn_upper        H_upper = diag(s) triu(Q^T A), masked to j >= i         (:186,195)
+#include "../../include/rnrqr.h"
+#include "common.hpp"
+#include "gemm_tn.hpp"
+#include "lu.hpp"
+#include "chol.hpp"
+#include "trsm.hpp"
+
+using namespace rnr;
+
+namespace {
+
+constexpr size_t kLdsMax = 160 * 1024;
+
+inline size_t up256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct Ws {
+  float* W;
+  float* L;
+  float* G;
+  float* Qb;
+  float* Dinv;
+  float* s;
+  int* perm;
+  int* info;
+};
+
+enum WsNeed : unsigned {
+  kNeedW = 1u, kNeedL = 2u, kNeedG = 4u, kNeedQb = 8u, kNeedDinv = 16u,
+  kNeedS = 32u, kNeedPerm = 64u, kNeedInfo = 128u
+};
+
+// Carves the workspace; returns the bytes needed.  With base == nullptr only sizes.
+size_t carve(int64_t batch, int64_t n, unsigned need, char* base, Ws* ws) {
+  const size_t nn = (size_t)batch * n * n * sizeof(float);
+  size_t off = 0;
+  auto take = [&](unsigned bit, size_t bytes) -> char* {
+    if (!(need & bit)) return nullptr;
+    char* p = base ? base + off : nullptr;
+    off += up256(bytes);
+    return p;
+  };
+  Ws w;
+  w.W = reinterpret_cast<float*>(take(kNeedW, nn));
+  w.L = reinterpret_cast<float*>(take(kNeedL, nn));
+  w.G = reinterpret_cast<float*>(take(kNeedG, nn));
+  w.Qb = reinterpret_cast<float*>(take(kNeedQb, nn));
+  w.Dinv = reinterpret_cast<float*>(take(kNeedDinv, (size_t)batch * n * 64 * sizeof(float)));
+  w.s = reinterpret_cast<float*>(take(kNeedS, (size_t)batch * n * sizeof(float)));
+  w.perm = reinterpret_cast<int*>(take(kNeedPerm, (size_t)batch * n * sizeof(int)));
+  w.info = reinterpret_cast<int*>(take(kNeedInfo, (size_t)batch * sizeof(int)));
+  if (ws) *ws = w;
+  return off;
+}
+
+constexpr unsigned kQrNeed = kNeedW | kNeedL | kNeedG | kNeedQb | kNeedDinv | kNeedS | kNeedPerm | kNeedInfo;
+constexpr unsigned kLuNeed = kNeedW;
+constexpr unsigned kCholqrNeed = kNeedG | kNeedDinv | kNeedInfo;
+constexpr unsigned kFrameNeed = kNeedW | kNeedL | kNeedG | kNeedDinv | kNeedPerm | kNeedInfo;
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_common(int64_t batch, int64_t n) {
+  if (batch < 0 || n < 0) return RNR_ERR_INVALID_ARG;
+  if (n < 1 || n > RNR_MAX_N) return RNR_ERR_UNSUPPORTED_N;
+  if (batch > (int64_t)INT32_MAX / 64) return RNR_ERR_INVALID_ARG;
+  return RNR_OK;
+}
+
+int lu_panel_width(int n) {
+  for (int nb = 64; nb >= 8; nb >>= 1)
+    if (lu_lds_bytes(n, nb) <= kLdsMax) return nb;
+  return 0;
+}
+
+int hip_status() { return hipGetLastError() == hipSuccess ? RNR_OK : RNR_ERR_HIP; }
+
+template <typename K>
+int set_lds(K kernel, size_t bytes) {
+  if (bytes <= 64 * 1024) return RNR_OK;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess
+             ? RNR_OK
+             : RNR_ERR_HIP;
+}
+
+int launch_lu(bool pivot, const float* src, int64_t ss, float* dst, int64_t sd, int64_t batch,
+              int n, int* perm, float* L, float* s, float* tau, hipStream_t st) {
+  LuArgs a;
+  a.src = src; a.ss = ss; a.dst = dst; a.sd = sd; a.n = n; a.nb = lu_panel_width(n);
+  a.perm = perm; a.L = L; a.sl = (int64_t)n * n; a.s = s; a.tau = tau;
+  if (a.nb == 0) return RNR_ERR_UNSUPPORTED_N;
+  const size_t lds = lu_lds_bytes(n, a.nb);
+  if (pivot) {
+    if (int e = set_lds(k_lu<true>, lds)) return e;
+    k_lu<true><<<dim3((unsigned)batch), dim3(kLuThreads), lds, st>>>(a);
+  } else {
+    if (int e = set_lds(k_lu<false>, lds)) return e;
+    k_lu<false><<<dim3((unsigned)batch), dim3(kLuThreads), lds, st>>>(a);
+  }
+  return hip_status();
+}
+
+// C[b] upper tiles of X^T Y (see gemm_tn.hpp); closure = masked + row-scaled.
+int launch_tn(bool closure, const float* X, int64_t sx, const float* Y, int64_t sy, float* C,
+              int64_t sc, const float* rs, int64_t batch, int n, bool klo_from_j, hipStream_t st) {
+  const bool big = n > 256;
+  const int BM = big ? 128 : 64;
+  TnArgs a;
+  a.X = X; a.sx = sx; a.Y = Y; a.sy = sy; a.C = C; a.sc = sc; a.rs = rs; a.n = n;
+  a.nt = (n + BM - 1) / BM;
+  a.ntiles = a.nt * (a.nt + 1) / 2;
+  a.klo_from_j = klo_from_j ? 1 : 0;
+  const int64_t total = batch * a.ntiles;
+  if (total > INT32_MAX) return RNR_ERR_INVALID_ARG;
+  a.total = (int)total;
+  const bool vec4 = (n % 4 == 0) && (sx % 4 == 0) && (sy % 4 == 0) && aligned(X, 16) && aligned(Y, 16);
+  const dim3 grid((unsigned)total), block(256);
+#define RNR_TN(BMv, MASK, RS, V) k_tn_upper<BMv, MASK, RS, V><<<grid, block, 0, st>>>(a)
+  if (closure) {
+    if (big) { if (vec4) RNR_TN(128, true, true, true); else RNR_TN(128, true, true, false); }
+    else     { if (vec4) RNR_TN(64, true, true, true);  else RNR_TN(64, true, true, false); }
+  } else {
+    if (big) { if (vec4) RNR_TN(128, false, false, true); else RNR_TN(128, false, false, false); }
+    else     { if (vec4) RNR_TN(64, false, false, true);  else RNR_TN(64, false, false, false); }
+  }
+#undef RNR_TN
+  return hip_status();
+}
+
+int launch_chol(float* G, int64_t sg, float* Dinv, int* info, int64_t batch, int n, bool keep_info,
+                hipStream_t st) {
+  CholArgs a;
+  a.G = G; a.sg = sg; a.Dinv = Dinv; a.info = info; a.n = n; a.keep_info = keep_info ? 1 : 0;
+  a.strip_lds = chol_lds_bytes(n, true) <= kLdsMax ? 1 : 0;
+  const size_t lds = chol_lds_bytes(n, a.strip_lds != 0);
+  if (int e = set_lds(k_chol, lds)) return e;
+  k_chol<<<dim3((unsigned)batch), dim3(kCholThreads), lds, st>>>(a);
+  return hip_status();
+}
+
+int launch_trsm(const float* M, int64_t sm, const float* R, int64_t sr, const float* Dinv, float* Q,
+                int64_t sq, float* Q2, int64_t sq2, const int* perm, int64_t batch, int n,
+                hipStream_t st) {
+  TrsmArgs a;
+  a.M = M; a.sm = sm; a.R = R; a.sr = sr; a.Dinv = Dinv; a.Q = Q; a.sq = sq; a.Q2 = Q2; a.sq2 = sq2;
+  a.perm = perm; a.n = n; a.nrb = (n + 63) / 64;
+  const int64_t total = batch * a.nrb;
+  if (total > INT32_MAX) return RNR_ERR_INVALID_ARG;
+  a.total = (int)total;
+  const bool vec4 = (n % 4 == 0) && (sq % 4 == 0) && (sr % 4 == 0) && aligned(Q, 16) && aligned(R, 16);
+  if (vec4)
+    k_trsm<true><<<dim3((unsigned)total), dim3(256), 0, st>>>(a);
+  else
+    k_trsm<false><<<dim3((unsigned)total), dim3(256), 0, st>>>(a);
+  return hip_status();
+}
+
+// One CholeskyQR pass: Q = M chol(M^T M + mu I)^-1, R left in G.
+int cholqr_pass(const float* M, int64_t sm, bool m_unit_lower, float* G, float* Dinv, int* info,
+                bool keep_info, float* Q, float* Q2, const int* perm, int64_t batch, int n,
+                hipStream_t st) {
+  const int64_t nn = (int64_t)n * n;
+  if (int e = launch_tn(false, M, sm, M, sm, G, nn, nullptr, batch, n, m_unit_lower, st)) return e;
+  if (int e = launch_chol(G, nn, Dinv, info, batch, n, keep_info, st)) return e;
+  return launch_trsm(M, sm, G, nn, Dinv, Q, nn, Q2, nn, perm, batch, n, st);
+}
+
+// The frame: LU of A into ws.W / ws.L / ws.perm, CholeskyQR2 of L, Q = P Q2 -> Q (and Q2).
+int frame(const float* A, int64_t sa, const Ws& w, float* Q, float* Qcopy, int* info, int64_t batch,
+          int n, hipStream_t st) {
+  const int64_t nn = (int64_t)n * n;
+  if (int e = launch_lu(true, A, sa, w.W, nn, batch, n, w.perm, w.L, nullptr, nullptr, st)) return e;
+  if (int e = cholqr_pass(w.L, nn, true, w.G, w.Dinv, info, false, w.W, nullptr, nullptr, batch, n, st))
+    return e;
+  return cholqr_pass(w.W, nn, false, w.G, w.Dinv, info, true, Q, Qcopy, w.perm, batch, n, st);
+}
+
+int check_ws(void* ws, size_t ws_bytes, size_t need) {
+  if (need == 0) return RNR_OK;
+  if (!ws || ws_bytes < need) return RNR_ERR_WORKSPACE;
+  if (!aligned(ws, 256)) return RNR_ERR_MISALIGNED;
+  return RNR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* rnr_status_string(int status) {
+  switch (status) {
+    case RNR_OK: return "success";
+    case RNR_ERR_INVALID_ARG: return "invalid argument (null pointer, negative size or stride < n*n)";
+    case RNR_ERR_UNSUPPORTED_N: return "unsupported matrix size (need 1 <= n <= 2048)";
+    case RNR_ERR_WORKSPACE: return "workspace missing or smaller than the size query returned";
+    case RNR_ERR_HIP: return "HIP launch or attribute call failed";
+    case RNR_ERR_MISALIGNED: return "misaligned pointer (data: 4 bytes, workspace: 256 bytes)";
+    default: return "unknown status";
+  }
+}
+
+const char* rnr_version(void) { return "0.1.0"; }
+
+int rnr_qr_f32_workspace(int64_t batch, int64_t n, size_t* bytes) {
+  if (!bytes) return RNR_ERR_INVALID_ARG;
+  if (int e = check_common(batch, n)) return e;
+  *bytes = batch == 0 ? 0 : carve(batch, n, kQrNeed, nullptr, nullptr);
+  return RNR_OK;
+}
+
+int rnr_qr_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride, float* H, float* tau,
+               int32_t* info, void* ws, size_t ws_bytes, rnr_stream_t stream) {
+  if (int e = check_common(batch, n)) return e;
+  if (batch == 0) return RNR_OK;
+  if (!A || !H || !tau || batch_stride < n * n) return RNR_ERR_INVALID_ARG;
+  if (!aligned(A, 4) || !aligned(H, 4) || !aligned(tau, 4)) return RNR_ERR_MISALIGNED;
+  const size_t need = carve(batch, n, kQrNeed, nullptr, nullptr);
+  if (int e = check_ws(ws, ws_bytes, need)) return e;
+  Ws w;
+  carve(batch, n, kQrNeed, static_cast<char*>(ws), &w);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int ni = (int)n;
+  const int64_t nn = n * n;
+  int* inf = info ? info : w.info;
+  if (int e = frame(A, batch_stride, w, w.Qb, H, inf, batch, ni, st)) return e;
+  if (int e = launch_lu(false, H, nn, H, nn, batch, ni, nullptr, nullptr, w.s, tau, st)) return e;
+  return launch_tn(true, w.Qb, nn, A, batch_stride, H, nn, w.s, batch, ni, false, st);
+}
+
+int rnr_lu_f32_workspace(int64_t batch, int64_t n, size_t* bytes) {
+  if (!bytes) return RNR_ERR_INVALID_ARG;
+  if (int e = check_common(batch, n)) return e;
+  *bytes = batch == 0 ? 0 : carve(batch, n, kLuNeed, nullptr, nullptr);
+  return RNR_OK;
+}
+
+int rnr_lu_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride, float* L, int32_t* perm,
+               void* ws, size_t ws_bytes, rnr_stream_t stream) {
+  if (int e = check_common(batch, n)) return e;
+  if (batch == 0) return RNR_OK;
+  if (!A || !L || !perm || batch_stride < n * n) return RNR_ERR_INVALID_ARG;
+  if (!aligned(A, 4) || !aligned(L, 4) || !aligned(perm, 4)) return RNR_ERR_MISALIGNED;
+  const size_t need = carve(batch, n, kLuNeed, nullptr, nullptr);
+  if (int e = check_ws(ws, ws_bytes, need)) return e;
+  Ws w;
+  carve(batch, n, kLuNeed, static_cast<char*>(ws), &w);
+  return launch_lu(true, A, batch_stride, w.W, n * n, batch, (int)n, perm, L, nullptr, nullptr,
+                   reinterpret_cast<hipStream_t>(stream));
+}
+
+int rnr_cholqr_f32_workspace(int64_t batch, int64_t n, size_t* bytes) {
+  if (!bytes) return RNR_ERR_INVALID_ARG;
+  if (int e = check_common(batch, n)) return e;
+  *bytes = batch == 0 ? 0 : carve(batch, n, kCholqrNeed, nullptr, nullptr);
+  return RNR_OK;
+}
+
+int rnr_cholqr_f32(const float* M, int64_t batch, int64_t n, int64_t batch_stride, float* Q, float* R,
+                   int32_t* info, void* ws, size_t ws_bytes, rnr_stream_t stream) {
+  if (int e = check_common(batch, n)) return e;
+  if (batch == 0) return RNR_OK;
+  if (!M || !Q || batch_stride < n * n) return RNR_ERR_INVALID_ARG;
+  if (!aligned(M, 4) || !aligned(Q, 4) || (R && !aligned(R, 4))) return RNR_ERR_MISALIGNED;
+  const size_t need = carve(batch, n, kCholqrNeed, nullptr, nullptr);
+  if (int e = check_ws(ws, ws_bytes, need)) return e;
+  Ws w;
+  carve(batch, n, kCholqrNeed, static_cast<char*>(ws), &w);
+  float* G = R ? R : w.G;
+  return cholqr_pass(M, batch_stride, false, G, w.Dinv, info ? info : w.info, false, Q, nullptr,
+                     nullptr, batch, (int)n, reinterpret_cast<hipStream_t>(stream));
+}
+
+int rnr_frame_f32_workspace(int64_t batch, int64_t n, size_t* bytes) {
+  if (!bytes) return RNR_ERR_INVALID_ARG;
+  if (int e = check_common(batch, n)) return e;
+  *bytes = batch == 0 ? 0 : carve(batch, n, kFrameNeed, nullptr, nullptr);
+  return RNR_OK;
+}
+
+int rnr_frame_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride, float* Q, int32_t* info,
+                  void* ws, size_t ws_bytes, rnr_stream_t stream) {
+  if (int e = check_common(batch, n)) return e;
+  if (batch == 0) return RNR_OK;
+  if (!A || !Q || batch_stride < n * n) return RNR_ERR_INVALID_ARG;
+  if (!aligned(A, 4) || !aligned(Q, 4)) return RNR_ERR_MISALIGNED;
+  const size_t need = carve(batch, n, kFrameNeed, nullptr, nullptr);
+  if (int e = check_ws(ws, ws_bytes, need)) return e;
+  Ws w;
+  carve(batch, n, kFrameNeed, static_cast<char*>(ws), &w);
+  return frame(A, batch_stride, w, Q, nullptr, info ? info : w.info, batch, (int)n,
+               reinterpret_cast<hipStream_t>(stream));
+}
+
+int rnr_chart_f32(float* Y, int64_t batch, int64_t n, float* s, float* tau, rnr_stream_t stream) {
+  if (int e = check_common(batch, n)) return e;
+  if (batch == 0) return RNR_OK;
+  if (!Y || !s || !tau) return RNR_ERR_INVALID_ARG;
+  if (!aligned(Y, 4) || !aligned(s, 4) || !aligned(tau, 4)) return RNR_ERR_MISALIGNED;
+  const int64_t nn = n * n;
+  return launch_lu(false, Y, nn, Y, nn, batch, (int)n, nullptr, nullptr, s, tau,
+                   reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+"""The C ABI without a GPU: the library loads, exports every function the header declares,
+and rejects bad arguments before it launches anything.  Also the host-side checks of the
+Python layer (no CPU fallback, shape validation)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT, load_package
+
+HEADER = os.path.join(ROOT, "include", "rnrqr.h")
+
+
+@pytest.fixture(scope="module")
+def native():
+    import importlib
+    load_package()
+    return importlib.import_module("qr-contest_amd._native")
+
+
+@pytest.fixture(scope="module")
+def lib(native):
+    return native.lib()
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(rnr_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_abi():
+    names = _declared()
+    for want in ("rnr_qr_f32", "rnr_qr_f32_workspace", "rnr_status_string", "rnr_lu_f32",
+                 "rnr_cholqr_f32", "rnr_frame_f32", "rnr_chart_f32"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol(lib, native):
+    names = _declared()
+    assert names, "no declarations parsed"
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in native.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_status_strings(lib, native):
+    for code in range(6):
+        assert native.status_string(code)
+    assert native.status_string(0) == "success"
+    assert "unknown" in native.status_string(99)
+    assert lib.rnr_version().decode().count(".") == 2
+
+
+def test_workspace_queries(native, lib):
+    assert native.workspace_bytes("qr", 0, 64) == 0
+    a = native.workspace_bytes("qr", 4, 64)
+    b = native.workspace_bytes("qr", 8, 64)
+    assert 0 < a < b
+    # four n*n float buffers per matrix at least
+    assert a >= 4 * 4 * 64 * 64 * 4
+    for kind in ("lu", "cholqr", "frame"):
+        assert native.workspace_bytes(kind, 3, 100) > 0
+    out = ctypes.c_size_t(0)
+    assert lib.rnr_qr_f32_workspace(4, 0, ctypes.byref(out)) == native.RNR_ERR_UNSUPPORTED_N
+    assert lib.rnr_qr_f32_workspace(4, 2049, ctypes.byref(out)) == native.RNR_ERR_UNSUPPORTED_N
+    assert lib.rnr_qr_f32_workspace(-1, 8, ctypes.byref(out)) == native.RNR_ERR_INVALID_ARG
+    assert lib.rnr_qr_f32_workspace(4, 8, None) == native.RNR_ERR_INVALID_ARG
+
+
+def test_argument_validation_before_any_launch(native, lib):
+    """Every call here must return an error without touching the device."""
+    fake = 1 << 20  # never dereferenced: validation fails first
+    need = native.workspace_bytes("qr", 2, 16)
+    f = lib.rnr_qr_f32
+    assert f(None, 2, 16, 256, fake, fake, None, fake, need, None) == native.RNR_ERR_INVALID_ARG
+    assert f(fake, 2, 16, 255, fake, fake, None, fake, need, None) == native.RNR_ERR_INVALID_ARG
+    assert f(fake, 2, 0, 256, fake, fake, None, fake, need, None) == native.RNR_ERR_UNSUPPORTED_N
+    assert f(fake, 2, 4096, 4096 ** 2, fake, fake, None, fake, need, None) == native.RNR_ERR_UNSUPPORTED_N
+    assert f(fake, 2, 16, 256, fake, fake, None, fake, need - 1, None) == native.RNR_ERR_WORKSPACE
+    assert f(fake, 2, 16, 256, fake, fake, None, None, need, None) == native.RNR_ERR_WORKSPACE
+    assert f(fake, 2, 16, 256, fake, fake, None, fake + 4, need, None) == native.RNR_ERR_MISALIGNED
+    assert f(fake + 2, 2, 16, 256, fake, fake, None, fake, need, None) == native.RNR_ERR_MISALIGNED
+    # batch 0 is a no-op that succeeds with null pointers
+    assert f(None, 0, 16, 256, None, None, None, None, 0, None) == native.RNR_OK
+    assert lib.rnr_chart_f32(None, 2, 8, fake, fake, None) == native.RNR_ERR_INVALID_ARG
+    assert lib.rnr_lu_f32(fake, 2, 8, 64, fake, None, fake, 1 << 30, None) == native.RNR_ERR_INVALID_ARG
+    assert lib.rnr_cholqr_f32(fake, 2, 8, 64, None, None, None, fake, 1 << 30, None) == native.RNR_ERR_INVALID_ARG
+
+
+def test_python_layer_rejects_cpu_and_non_square(pkg):
+    with pytest.raises(RuntimeError, match="GPU only"):
+        pkg.custom_kernel(torch.randn(2, 8, 8))
+    with pytest.raises(ValueError):
+        pkg.custom_kernel(torch.randn(2, 8, 7))
+    with pytest.raises(ValueError):
+        pkg.custom_kernel(torch.randn(8))
+
+
+def test_build_command_targets_gfx950_without_packed_fp32(pkg):
+    import importlib
+    b = importlib.import_module("qr-contest_amd.build")
+    cmd = b.command("/tmp/x.so")
+    assert "--offload-arch=gfx950" in cmd
+    i = cmd.index("-packed-fp32-ops")
+    assert cmd[i - 1] == "-Xclang" and cmd[i - 2] == "-target-feature"
