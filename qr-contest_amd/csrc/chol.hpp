@@ -2,15 +2,18 @@
 //
 //   mu = 1e-7 * mean(diag G);  G += mu I;  G = R^T R        -- reflection_no_reflectors.py:74-76
 //
-// Blocked right-looking with 64-column blocks.  For block k the diagonal block is
-// factored in LDS (two barriers per column), its inverse Dinv_kk = R_kk^-1 is formed in
-// LDS (8 lanes per column, back substitution, no workgroup barriers), the block row
-// R_k,> = Dinv_kk^T G_k,> and the trailing update G_>,> -= R_k,>^T R_k,> (upper tiles
-// only) run on MFMA, each wave owning whole output tiles.  When the block row fits it
-// is also kept in LDS for the trailing update (n <= 576), otherwise it is read back
-// from G.  The diagonal-block inverses go to Dinv ([n][64] per matrix) for the
-// triangular solve that follows.  info records the first column whose pivot was not
-// positive (1-based; NaN counts as not positive).
+// Blocked right-looking with 64-column blocks.  For block k:
+//   * wave 0 factors the diagonal block with one symmetric row per lane in registers and
+//     the scaled pivot row broadcast through LDS inside the wave (no barriers or fences);
+//   * every wave then forms 8 columns of Dinv_kk = R_kk^-1 by back substitution, one row
+//     per lane in registers, readlane broadcasts; Dinv_kk^T is staged in LDS;
+//   * the block row R_k,> = Dinv_kk^T G_k,> and the trailing update G_>,> -= R_k,>^T R_k,>
+//     (upper 64x64 tiles only) run on MFMA, each wave owning whole output tiles.  When the
+//     block row fits it is also kept in LDS for the trailing update (n <= 576), otherwise
+//     it is read back from G.
+// The diagonal-block inverses go to Dinv ([n][64] per matrix) for the triangular solve
+// that follows.  info records the first column whose pivot was not positive (1-based; NaN
+// counts as not positive).
 #pragma once
 #include "common.hpp"
 
@@ -31,14 +34,16 @@ constexpr int kCholNb = 64;
 
 inline size_t chol_lds_bytes(int n, bool strip) {
   const size_t w = n > kCholNb ? (size_t)(n - kCholNb) : 1;
-  return sizeof(float) * (64 * 65 + 64 + 32 + (strip ? 64 * w : 0));
+  return sizeof(float) * (2 * 64 * 65 + 64 + 32 + (strip ? 64 * w : 0));
 }
 
 __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
-  extern __shared__ float smem[];
-  float* D = smem;                 // [64][65]: upper = R_kk, strict lower = (R_kk^-1)^T
-  float* xd = D + 64 * 65;         // diagonal of R_kk^-1
-  float* red = xd + 64;            // [16]
+  constexpr int NW = kCholThreads / 64, CPW = 64 / NW;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* D = smem;                 // [64][65] diagonal block, then R_kk (upper, zero below)
+  float* XT = D + 64 * 65;         // [64][65] (R_kk^-1)^T: XT[i][k] = Dinv_kk[k][i]
+  float* SB = XT + 64 * 65;        // [64] scaled pivot row broadcast (wave 0)
+  float* red = SB + 64;            // [16]
   int* ffail = reinterpret_cast<int*>(red + 16);
   float* S = red + 32;             // block row [64][n-64] when strip_lds
 
@@ -58,7 +63,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
   __syncthreads();
   float tot = 0.f;
 #pragma unroll
-  for (int w = 0; w < kCholThreads / 64; ++w) tot += red[w];
+  for (int w = 0; w < NW; ++w) tot += red[w];
   const float mu = 1e-7f * (tot / (float)n);
   for (int i = tid; i < n; i += kCholThreads) G[(int64_t)i * n + i] += mu;
   __syncthreads();
@@ -66,57 +71,105 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
   for (int k0 = 0; k0 < n; k0 += kCholNb) {
     const int kb = min(kCholNb, n - k0), k1 = k0 + kb, w = n - k1;
 
+    // diagonal block (upper part as stored); outside kb an identity pads it
     for (int idx = tid; idx < 64 * 64; idx += kCholThreads) {
       const int i = idx >> 6, c = idx & 63;
-      D[i * 65 + c] = (i < kb && c < kb && c >= i) ? G[(int64_t)(k0 + i) * n + k0 + c] : 0.f;
+      float v = (i == c) ? 1.f : 0.f;
+      if (i < kb && c < kb && c >= i) v = G[(int64_t)(k0 + i) * n + k0 + c];
+      D[i * 65 + c] = v;
     }
     __syncthreads();
 
-    // unblocked upper Cholesky of the diagonal block
-    for (int j = 0; j < kb; ++j) {
-      const float d = D[j * 65 + j];
-      if (tid == 0 && !(d > 0.f) && *ffail == INT_MAX) *ffail = k0 + j + 1;
-      const float r = sqrtf(d);
-      const float rinv = 1.f / r;
-      for (int c = j + 1 + tid; c < kb; c += kCholThreads) D[j * 65 + c] *= rinv;
-      __syncthreads();
-      const int t = kb - j - 1;
-      for (int idx = tid; idx < t * t; idx += kCholThreads) {
-        const int ra = idx / t, rc = idx - ra * t;
-        if (rc >= ra) {
-          const int ia = j + 1 + ra, ic = j + 1 + rc;
-          D[ia * 65 + ic] -= D[j * 65 + ia] * D[j * 65 + ic];
+    if (wid == 0) {
+      // lane i holds symmetric row i of the block; step j broadcasts the scaled pivot row
+      // R[j][c] = G'[j][c] / r (held by lane c) through LDS inside the wave.  A wave issues
+      // its LDS operations in order and the store/load addresses may alias, so neither the
+      // hardware nor the compiler reorders them: no fence or barrier sits on the chain.
+      // the row is four named 16-wide vectors (element access with compile-time indices), so
+      // it stays in VGPRs whatever the unrolled code around it looks like
+      f32x16 v0, v1, v2, v3;
+      auto V = [&](auto qc) -> f32x16& {
+        constexpr int q = decltype(qc)::value;
+        if constexpr (q == 0) return v0;
+        else if constexpr (q == 1) return v1;
+        else if constexpr (q == 2) return v2;
+        else return v3;
+      };
+      static_for<0, 4>([&](auto qc) {
+        constexpr int q = decltype(qc)::value;
+        f32x16& v = V(qc);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int c = 16 * q + e;
+          v[e] = D[(c >= lane) ? lane * 65 + c : c * 65 + lane];
         }
-      }
-      if (tid == 0) D[j * 65 + j] = r;
-      __syncthreads();
-    }
-
-    // Dinv_kk = R_kk^-1 (upper), column j by the 8 lanes of group j; X[i][j] (i < j)
-    // is kept as D[j][i] and X[j][j] as xd[j].
-    {
-      const int j = tid >> 3, sub = tid & 7;
-      if (j < kb) {
-        const float xjj = 1.f / D[j * 65 + j];
-        if (sub == 0) xd[j] = xjj;
-        for (int i = j - 1; i >= 0; --i) {
-          float s = 0.f;
-          for (int q = i + 1 + sub; q <= j; q += 8) {
-            const float xq = (q == j) ? xjj : D[j * 65 + q];
-            s += D[i * 65 + q] * xq;
+      });
+      int fail = INT_MAX;
+      static_for<0, 64>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const float rjj = V(std::integral_constant<int, j / 16>{})[j % 16];
+        const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rjj), j));
+        if (!(d > 0.f) && fail == INT_MAX) fail = j;
+        const float r = sqrtf(d), rinv = 1.f / r;
+        const float si = (ln == j) ? r : rjj * rinv;  // lane c > j: R[j][c]
+        const float sm = (ln > j) ? si : 0.f;          // rows below j take the update
+        SB[ln] = si;
+        // 16 broadcast values at a time (scheduling barriers keep the reads from all being
+        // hoisted at once)
+        static_for<(j + 1) / 16, 4>([&](auto qc) {
+          constexpr int q = decltype(qc)::value;
+          f32x16& v = V(qc);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            if (16 * q + e > j) v[e] -= sm * SB[16 * q + e];
           }
-          s = group8_sum(s);
-          if (sub == 0) D[j * 65 + i] = -s / D[i * 65 + i];
-          wave_lds_order();
-        }
-      }
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        D[j * 65 + ln] = (ln >= j) ? si : 0.f;  // row j of R
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      if (lane == 0 && fail != INT_MAX && fail < kb && *ffail == INT_MAX) *ffail = k0 + fail + 1;
     }
     __syncthreads();
 
+    // Dinv_kk = R_kk^-1 by back substitution: wave w solves columns w*CPW.., lane i holding
+    // row i of R and entry i of the running right-hand side
+    {
+      float rr[64];
+#pragma unroll
+      for (int c = 0; c < 64; ++c) rr[c] = D[lane * 65 + c];  // R_kk is zero below the diagonal
+      const float rd = 1.f / D[lane * 65 + lane];  // 1 / R[i][i] in lane i
+      float x[CPW];
+      const int cw = __builtin_amdgcn_readfirstlane(wid * CPW);
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) x[u] = (lane == cw + u) ? 1.f : 0.f;
+      static_for<0, 64>([&](auto kc) {
+        constexpr int k = 63 - decltype(kc)::value;  // k = 63 .. 0
+        int ln = lane, c0w = cw;
+        asm volatile("" : "+v"(ln), "+s"(c0w));
+        const float rk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rd), k));
+        const float mr = (ln < k) ? rr[k] : 0.f;  // rows above k take the update
+#pragma unroll
+        for (int u = 0; u < CPW; ++u) {
+          if (k <= c0w + u) {
+            const float xk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[u]), k)) * rk;
+            x[u] = (ln == k) ? xk : x[u] - mr * xk;
+          }
+        }
+      });
+      // column cw+u of the inverse -> XT[cw+u][i]
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) XT[(cw + u) * 65 + lane] = (lane <= cw + u) ? x[u] : 0.f;
+    }
+    __syncthreads();
+
+    // R_kk (upper) and Dinv_kk (row-major, zero below the diagonal) to HBM
     for (int idx = tid; idx < kb * 64; idx += kCholThreads) {
       const int i = idx >> 6, c = idx & 63;
       if (c < kb && c >= i) G[(int64_t)(k0 + i) * n + k0 + c] = D[i * 65 + c];
-      Dv[(int64_t)(k0 + i) * 64 + c] = (c < kb) ? (c > i ? D[c * 65 + i] : (c == i ? xd[i] : 0.f)) : 0.f;
+      Dv[(int64_t)(k0 + i) * 64 + c] = (c < kb) ? XT[c * 65 + i] : 0.f;
     }
     if (w <= 0) break;  // uniform; kb == 64 below this line
 
@@ -124,17 +177,18 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
     // so it can overwrite them in G without racing other waves' reads.
     {
       const int nch = (w + 31) >> 5;
-      for (int job = wid; job < nch; job += kCholThreads / 64) {
+      for (int job = wid; job < nch; job += NW) {
         const int colr = job * 32 + l32, col = k1 + colr;
+        float bv[32];
+#pragma unroll
+        for (int t = 0; t < 32; ++t)
+          bv[t] = (col < n) ? G[(int64_t)(k0 + 2 * t + h) * n + col] : 0.f;
         f32x16 acc0 = zero16(), acc1 = zero16();
-        for (int kk = 0; kk < kCholNb; kk += 2) {
-          const int k = kk + h;
-          const float bv = (col < n) ? G[(int64_t)(k0 + k) * n + col] : 0.f;
-          const int ia = l32, ib = 32 + l32;
-          const float a0 = (k < ia) ? D[ia * 65 + k] : (k == ia ? xd[ia] : 0.f);
-          const float a1 = (k < ib) ? D[ib * 65 + k] : (k == ib ? xd[ib] : 0.f);
-          acc0 = mfma(a0, bv, acc0);
-          acc1 = mfma(a1, bv, acc1);
+#pragma unroll
+        for (int t = 0; t < 32; ++t) {
+          const int k = 2 * t + h;
+          acc0 = mfma(XT[l32 * 65 + k], bv[t], acc0);
+          acc1 = mfma(XT[(32 + l32) * 65 + k], bv[t], acc1);
         }
         if (col < n) {
 #pragma unroll
@@ -155,7 +209,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
     // trailing G_>,> -= R_k,>^T R_k,> over upper 64x64 tiles, one tile per wave at a time
     {
       const int nt = (w + 63) >> 6, npairs = nt * (nt + 1) / 2;
-      for (int pr = wid; pr < npairs; pr += kCholThreads / 64) {
+      for (int pr = wid; pr < npairs; pr += NW) {
         int I, J;
         upper_tile(pr, nt, I, J);
         f32x16 acc[2][2];
@@ -169,6 +223,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
               const int col = k1 + J * 64 + nj * 32 + l32;
               acc[mi][nj][r] = (row < n && col < n) ? G[(int64_t)row * n + col] : 0.f;
             }
+#pragma unroll 4
         for (int kk = 0; kk < kCholNb; kk += 2) {
           const int k = kk + h;
           float av[2], bv[2];

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <limits.h>
+#include <type_traits>
 
 namespace rnr {
 
@@ -51,6 +52,67 @@ __device__ __forceinline__ float group8_sum(float v) {
   v += __shfl_xor(v, 2);
   v += __shfl_xor(v, 4);
   return v;
+}
+
+// DPP lane permutations within rows of 16 lanes (VALU, no LDS round trip).
+constexpr int kDppQuad1032 = 0xB1;      // lane ^ 1
+constexpr int kDppQuad2301 = 0x4E;      // lane ^ 2
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <-> 7 - i within 8
+constexpr int kDppRowMirror = 0x140;      // lane i <-> 15 - i within 16
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// One combine step of the first-maximum argmax: larger |value| wins, equal |value| goes to
+// the smaller index.
+__device__ __forceinline__ void argmax_take(float& babs, float& bv, int& bi, float oabs, float ov, int oi) {
+  const bool take = (oabs > babs) | ((oabs == babs) & (oi < bi));  // branch-free
+  babs = take ? oabs : babs;
+  bv = take ? ov : bv;
+  bi = take ? oi : bi;
+}
+
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp_step(float& babs, float& bv, int& bi) {
+  argmax_take(babs, bv, bi, dpp_f<CTRL>(babs), dpp_f<CTRL>(bv), dpp_i<CTRL>(bi));
+}
+
+// Wave-wide first-maximum argmax of (|v|, index); every lane gets the wave's winner.
+// Four DPP steps reduce each row of 16 lanes, the four rows are combined by readlane.
+__device__ __forceinline__ void wave_argmax(float& babs, float& bv, int& bi) {
+  argmax_dpp_step<kDppQuad1032>(babs, bv, bi);
+  argmax_dpp_step<kDppQuad2301>(babs, bv, bi);
+  argmax_dpp_step<kDppRowHalfMirror>(babs, bv, bi);
+  argmax_dpp_step<kDppRowMirror>(babs, bv, bi);
+  float ra = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(babs), 0));
+  float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 0));
+  int ri = __builtin_amdgcn_readlane(bi, 0);
+#pragma unroll
+  for (int row = 1; row < 4; ++row) {
+    const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(babs), 16 * row));
+    const float tv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 16 * row));
+    const int ti = __builtin_amdgcn_readlane(bi, 16 * row);
+    argmax_take(ra, rv, ri, t, tv, ti);
+  }
+  babs = ra;
+  bv = rv;
+  bi = ri;
+}
+
+// Calls f(std::integral_constant<int, I>) for I = B .. E-1, fully unrolled at compile time
+// (register arrays indexed by I then stay in registers).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 // Upper-triangular tile enumeration: t -> (ti, tj), ti <= tj < nt, row by row.

@@ -25,6 +25,8 @@ struct TnArgs {
   float* C;
   int64_t sc;
   const float* rs;  // row scale, batch stride n (ROW_SCALE only)
+  const int* lperm; // non-null: X = Y = unit-lower L stored in A's row order (the LU's
+                    // in-place factor); logical row r is physical row lperm[b][r]
   int n;
   int nt;       // tiles per matrix edge
   int ntiles;   // upper tiles per matrix
@@ -59,7 +61,48 @@ __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
     for (int nj = 0; nj < NB; ++nj) acc[mi][nj] = zero16();
 
   float rx[PER], ry[PER];
+  const int* lp = a.lperm ? a.lperm + (int64_t)b * n : nullptr;
+  // element (r, c) of the unit-lower view: below the diagonal from row lp[r], 1 on it, 0 above
+  auto lview4 = [&](int gr, int c) -> float4 {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c < gr) v = *reinterpret_cast<const float4*>(X + (int64_t)lp[gr] * n + c);
+    v.x = (c < gr) ? v.x : (c == gr ? 1.f : 0.f);
+    v.y = (c + 1 < gr) ? v.y : (c + 1 == gr ? 1.f : 0.f);
+    v.z = (c + 2 < gr) ? v.z : (c + 2 == gr ? 1.f : 0.f);
+    v.w = (c + 3 < gr) ? v.w : (c + 3 == gr ? 1.f : 0.f);
+    return v;
+  };
+  auto lview1 = [&](int gr, int c) -> float {
+    return (c < gr) ? X[(int64_t)lp[gr] * n + c] : (c == gr ? 1.f : 0.f);
+  };
   auto gload = [&](int k) {
+    if (lp) {
+      if constexpr (VEC4) {
+#pragma unroll
+        for (int p = 0; p < PER / 4; ++p) {
+          const int idx = tid + 256 * p;
+          const int row = idx / (BM / 4), c = 4 * (idx % (BM / 4));
+          const int gr = k + row;
+          float4 vx = make_float4(0.f, 0.f, 0.f, 0.f), vy = vx;
+          if (gr < n) {
+            if (i0 + c < n) vx = lview4(gr, i0 + c);
+            if (j0 + c < n) vy = lview4(gr, j0 + c);
+          }
+          rx[4 * p + 0] = vx.x; rx[4 * p + 1] = vx.y; rx[4 * p + 2] = vx.z; rx[4 * p + 3] = vx.w;
+          ry[4 * p + 0] = vy.x; ry[4 * p + 1] = vy.y; ry[4 * p + 2] = vy.z; ry[4 * p + 3] = vy.w;
+        }
+      } else {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+          const int idx = tid + 256 * p;
+          const int row = idx / BM, c = idx % BM;
+          const int gr = k + row;
+          rx[p] = (gr < n && i0 + c < n) ? lview1(gr, i0 + c) : 0.f;
+          ry[p] = (gr < n && j0 + c < n) ? lview1(gr, j0 + c) : 0.f;
+        }
+      }
+      return;
+    }
     if constexpr (VEC4) {
 #pragma unroll
       for (int p = 0; p < PER / 4; ++p) {

@@ -3,18 +3,25 @@
 // PIVOT = true : partial-pivot LU, A[perm] = L U (torch.linalg.lu / LAPACK getrf
 //                semantics, first maximum of |a_ij| wins) -- reflection_no_reflectors.py:66.
 //                Rows are never moved: a logical->physical row map (perm) is kept in LDS and
-//                every access goes through it, so the finished factor sits in A's own row
-//                order and one gather at the end writes L in pivoted order with a unit
-//                diagonal and exact zeros above it.  U is not kept: the reference drops it.
+//                every access goes through it, so the factor sits in A's own row order;
+//                consumers read L through perm (or one optional gather writes it out in
+//                pivoted order).  U is not kept: the reference drops it.
 // PIVOT = false: the chart, the sign-ruled unpivoted LU of I - Q S run on the Q copy
 //                (reflection_no_reflectors.py:139-174): s_k = +1 iff |1-d| >= |1+d|
 //                (:150-155), multipliers (-s_k M[i,k]) / pivot (:157-158), then
 //                tau_k = 2 / (1 + sum_{i>k} Y[i,k]^2) (:192).  Runs in place on H.
 //
-// Per panel of nb columns: the panel (rows k0..n) is factored in LDS; it is written back;
-// the unit-lower L11 is inverted in LDS; then, chunk by chunk of 64 trailing columns,
-// U12 = L11^-1 A12 and A22 -= L21 U12 run on MFMA.  Both trailing products read their
-// operands from LDS; only A22 itself streams through HBM/L2, once per panel.
+// Per panel of NB columns (NB = 64 / 32 / 16 for n <= 512 / 1024 / 2048):
+//   * the panel's rows live in registers, RPT rows per thread (one row per thread up to
+//     n = 512).  A column step of the LU is a DPP argmax per wave, one barrier, the pivot
+//     row broadcast through LDS, a second barrier and a register rank-1 update; the chart
+//     needs only the broadcast and one barrier;
+//   * the factored panel goes to LDS (row stride NB+1: conflict-free column reads, and a
+//     thread addresses its own row with one base register) and back to HBM;
+//   * X = L11^-1 is swept column by column inside each wave (readlane broadcasts, no
+//     barriers); per chunk of 64 trailing columns -U12 = -X A12 runs on 16x16x4 MFMA over
+//     all waves and A22 += L21 (-U12) on 32x32x2 MFMA, one 32-row tile per wave at a
+//     time.  Only A22 streams through HBM/L2.
 #pragma once
 #include "common.hpp"
 
@@ -25,9 +32,10 @@ struct LuArgs {
   int64_t ss;
   float* dst;        // working matrix (LU: workspace W; chart: H itself)
   int64_t sd;
-  int n, nb;
+  int n;
+  int vec4;          // n % 4 == 0 and src, dst 16-byte aligned (batch strides too)
   int* perm;         // PIVOT: logical -> original row, [batch][n]
-  float* L;          // PIVOT: unit-lower factor, [batch][n][n]
+  float* L;          // PIVOT: optional unit-lower factor in pivoted order, [batch][n][n]
   int64_t sl;
   float* s;          // chart: signs, [batch][n]
   float* tau;        // chart: tau, [batch][n]
@@ -35,122 +43,256 @@ struct LuArgs {
 
 constexpr int kLuThreads = 512;
 
-inline size_t lu_lds_bytes(int n, int nb) {
-  return sizeof(float) * ((size_t)n * (nb + 1) + (size_t)nb * 64 + (size_t)n + 32);
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16];
+// D[row][col] sits in lane col + 16 * (row / 4), register row % 4.
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-template <bool PIVOT>
+inline int lu_panel_nb(int n) { return n <= 512 ? 64 : (n <= 1024 ? 32 : 16); }
+
+inline size_t lu_lds_bytes(int n, int nb) {
+  return sizeof(float) * ((size_t)n * (nb + 1) + (size_t)nb * 64 + (size_t)n + 4);
+}
+
+template <bool PIVOT, int NB, int RPT>
 __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
-  extern __shared__ float smem[];
-  const int n = a.n, nb = a.nb, ldp = nb + 1;
-  float* P = smem;                                     // panel, n x (nb+1)
-  float* U = P + (size_t)n * ldp;                      // -U12 chunk [nb][64]; L11^-1 scratch
-  int* pl = reinterpret_cast<int*>(U + nb * 64);       // logical -> physical row
-  float* redv = reinterpret_cast<float*>(pl + n);      // pivot search, one entry per wave
-  int* redi = reinterpret_cast<int*>(redv + 8);
+  constexpr int T = kLuThreads, NW = T / 64;
+  constexpr int NB4 = NB / 4;
+  constexpr int LDP = NB + 1;
+  constexpr int CPW = NB / NW;       // columns of L11^-1 per wave
+  static_assert(NB % NW == 0 && NB <= 64, "panel width");
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int n = a.n;
+  float* P = smem;                                  // panel [n][NB+1]
+  float* U = P + (((size_t)n * LDP + 3) & ~(size_t)3);  // -U12 chunk [NB][64]; panel-phase scratch
+  int* pl = reinterpret_cast<int*>(U + NB * 64);    // logical -> physical row
+  float4* PB4 = reinterpret_cast<float4*>(U);       // [2][NB/4] pivot row
+  float4* PJ4 = PB4 + 2 * NB4;                      // [2][NB/4] displaced row j
+  float2* red = reinterpret_cast<float2*>(U + 4 * NB);  // [2][NW] (value, index bits)
 
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int l32 = lane & 31, h = lane >> 5;
+  const int l32 = lane & 31, h = lane >> 5, l16 = lane & 15, q4 = lane >> 4;
   const float* src = a.src + b * a.ss;
   float* dst = a.dst + b * a.sd;
+  auto sw = [](int r, int c) { return r * LDP + c; };
 
   if (PIVOT)
-    for (int i = tid; i < n; i += kLuThreads) pl[i] = i;
+    for (int i = tid; i < n; i += T) pl[i] = i;
   __syncthreads();
 
-  for (int k0 = 0; k0 < n; k0 += nb) {
-    const int kb = min(nb, n - k0), m = n - k0, k1 = k0 + kb;
+  for (int k0 = 0; k0 < n; k0 += NB) {
+    const int kb = min(NB, n - k0), m = n - k0, k1 = k0 + kb;
     const float* cur = (k0 == 0) ? src : dst;
 
-    // ---- load the panel: logical rows k0..n-1, columns k0..k0+nb (zero padded)
-    for (int idx = tid; idx < m * nb; idx += kLuThreads) {
-      const int r = idx / nb, c = idx - r * nb;
-      const int pr = PIVOT ? pl[k0 + r] : k0 + r;
-      P[r * ldp + c] = (c < kb) ? cur[(int64_t)pr * n + k0 + c] : 0.f;
-    }
-    __syncthreads();
-
-    // ---- factor the panel column by column
-    for (int j = 0; j < kb; ++j) {
-      if constexpr (PIVOT) {
-        // first maximum of |P[r][j]| over r in [j, m): per thread rows ascend, ties across
-        // threads and waves go to the smaller row index
-        float bv = 0.f, babs = -1.f;
-        int bi = INT_MAX;
-        for (int r = j + tid; r < m; r += kLuThreads) {
-          const float v = P[r * ldp + j];
-          const float av = fabsf(v);
-          if (av > babs) { babs = av; bv = v; bi = r; }
+    // ---- panel HBM -> LDS, four float4 loads in flight per thread
+    if (a.vec4) {
+      const int tot = m * NB4;
+      for (int f0 = tid; f0 < tot; f0 += 4 * T) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int f = f0 + T * u;
+          v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (f < tot) {
+            const int r = f / NB4, c = 4 * (f - r * NB4);
+            const int pr = PIVOT ? pl[k0 + r] : k0 + r;
+            if (c < kb) v[u] = *reinterpret_cast<const float4*>(cur + (int64_t)pr * n + k0 + c);
+          }
         }
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-          const float ob = __shfl_xor(babs, off);
-          const float ov = __shfl_xor(bv, off);
-          const int oi = __shfl_xor(bi, off);
-          if (ob > babs || (ob == babs && oi < bi)) { babs = ob; bv = ov; bi = oi; }
-        }
-        if (lane == 0) { redv[wid] = bv; redi[wid] = bi; }
-        __syncthreads();
-        float pv = 0.f, pabs = -1.f;
-        int p = INT_MAX;
-#pragma unroll
-        for (int w = 0; w < kLuThreads / 64; ++w) {
-          const float v = redv[w];
-          const int i = redi[w];
-          const float av = fabsf(v);
-          if (i != INT_MAX && (av > pabs || (av == pabs && i < p))) { pabs = av; pv = v; p = i; }
-        }
-        if (p == INT_MAX) { p = j; pv = P[j * ldp + j]; }   // only non-finite columns get here
-        if (p != j) {
-          for (int c = tid; c < nb; c += kLuThreads) {
-            const float t = P[j * ldp + c];
-            P[j * ldp + c] = P[p * ldp + c];
-            P[p * ldp + c] = t;
-          }
-          if (tid == 0) {
-            const int t = pl[k0 + j];
-            pl[k0 + j] = pl[k0 + p];
-            pl[k0 + p] = t;
+        for (int u = 0; u < 4; ++u) {
+          const int f = f0 + T * u;
+          if (f < tot) {
+            const int r = f / NB4, c = 4 * (f - r * NB4);
+            float* d = P + sw(r, c);
+            d[0] = v[u].x; d[1] = v[u].y; d[2] = v[u].z; d[3] = v[u].w;
           }
         }
-        __syncthreads();
-        // LAPACK xGETRF2: scale by the reciprocal unless the pivot is subnormal; a zero
-        // pivot leaves the column as it is (the update below is then a no-op).
-        const bool nz = pv != 0.f;
-        const bool recip = fabsf(pv) >= 1.17549435e-38f;
-        const float inv = 1.f / pv;
-        for (int r = j + 1 + tid; r < m; r += kLuThreads) {
-          float l = P[r * ldp + j];
-          if (nz) {
-            l = recip ? l * inv : l / pv;
-            P[r * ldp + j] = l;
-          }
-          for (int c = j + 1; c < kb; ++c) P[r * ldp + c] -= l * P[j * ldp + c];
-        }
-        __syncthreads();
-      } else {
-        const float d = P[j * ldp + j];
-        const float pp = 1.f - d, pm = 1.f + d;
-        const bool plus = fabsf(pp) >= fabsf(pm);
-        const float sk = plus ? 1.f : -1.f;
-        const float piv = plus ? pp : pm;
-        if (tid == 0) a.s[(int64_t)b * n + k0 + j] = sk;
-        for (int r = j + 1 + tid; r < m; r += kLuThreads) {
-          const float mult = (-sk * P[r * ldp + j]) / piv;
-          P[r * ldp + j] = mult;
-          for (int c = j + 1; c < kb; ++c) P[r * ldp + c] -= mult * P[j * ldp + c];
-        }
-        __syncthreads();
+      }
+    } else {
+      for (int idx = tid; idx < m * NB; idx += T) {
+        const int r = idx / NB, c = idx - r * NB;
+        const int pr = PIVOT ? pl[k0 + r] : k0 + r;
+        P[sw(r, c)] = (c < kb) ? cur[(int64_t)pr * n + k0 + c] : 0.f;
       }
     }
+    __syncthreads();
+    float row[RPT][NB];
+#pragma unroll
+    for (int q = 0; q < RPT; ++q) {
+      const int r = tid + T * q;
+#pragma unroll
+      for (int c = 0; c < NB; ++c) row[q][c] = (r < m) ? P[sw(r, c)] : 0.f;
+    }
+
+    // ---- factor the panel column by column (compile-time column index).  Columns past kb
+    //      (last panel only) are no-ops: rows >= m are zero and none is below row j >= m.
+    int buf = 0;
+    float my_s = 1.f;
+    static_for<0, NB>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      {
+        // the row index is laundered through an empty asm each column so that the per-column
+        // lane masks (r > j, r >= j) are formed here instead of being hoisted for all NB
+        // columns to the kernel start (which spills ~1000 SGPRs)
+        int rbase = tid;
+        asm volatile("" : "+v"(rbase));
+        float l[RPT];
+        if constexpr (PIVOT) {
+          float bv = 0.f, babs = -1.f;
+          int bi = INT_MAX;
+#pragma unroll
+          for (int q = 0; q < RPT; ++q) {
+            const int r = rbase + T * q;
+            const float v = row[q][j], av = fabsf(v);
+            if (r >= j && r < m && av > babs) { babs = av; bv = v; bi = r; }
+          }
+          wave_argmax(babs, bv, bi);
+          if (lane == 0) red[buf * NW + wid] = make_float2(bv, __int_as_float(bi));
+          __syncthreads();
+          // the NW wave winners in one batch of LDS reads, then a branch-free reduction
+          // (a wave without candidates reports index INT_MAX and ranks below any row)
+          float4 e4[NW / 2];
+#pragma unroll
+          for (int w = 0; w < NW / 2; ++w) e4[w] = reinterpret_cast<const float4*>(red + buf * NW)[w];
+          float pv = e4[0].x, pabs;
+          int p = __float_as_int(e4[0].y);
+          pabs = (p == INT_MAX) ? -1.f : fabsf(pv);
+#pragma unroll
+          for (int w = 1; w < NW; ++w) {
+            const float v = (w & 1) ? e4[w / 2].z : e4[w / 2].x;
+            const int i = __float_as_int((w & 1) ? e4[w / 2].w : e4[w / 2].y);
+            argmax_take(pabs, pv, p, (i == INT_MAX) ? -1.f : fabsf(v), v, i);
+          }
+          p = __builtin_amdgcn_readfirstlane(p);
+          pv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(pv)));
+          if (p == INT_MAX) { p = j; pv = __int_as_float(0x7fc00000); }  // all-NaN column
+          const int po = p % T, pq = p / T;
+          if (tid == po) {
+#pragma unroll
+            for (int q = 0; q < RPT; ++q)
+              if (q == pq) {
+#pragma unroll
+                for (int c4 = 0; c4 < NB4; ++c4)
+                  PB4[buf * NB4 + c4] = make_float4(row[q][4 * c4], row[q][4 * c4 + 1],
+                                                    row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
+              }
+          }
+          if (p != j && tid == j) {
+#pragma unroll
+            for (int c4 = 0; c4 < NB4; ++c4)
+              PJ4[buf * NB4 + c4] = make_float4(row[0][4 * c4], row[0][4 * c4 + 1],
+                                                row[0][4 * c4 + 2], row[0][4 * c4 + 3]);
+          }
+          __syncthreads();
+          if (p != j) {
+            if (tid == j) {
+#pragma unroll
+              for (int c4 = 0; c4 < NB4; ++c4) {
+                const float4 t = PB4[buf * NB4 + c4];
+                row[0][4 * c4] = t.x; row[0][4 * c4 + 1] = t.y;
+                row[0][4 * c4 + 2] = t.z; row[0][4 * c4 + 3] = t.w;
+              }
+            }
+            if (tid == po) {
+#pragma unroll
+              for (int q = 0; q < RPT; ++q)
+                if (q == pq) {
+#pragma unroll
+                  for (int c4 = 0; c4 < NB4; ++c4) {
+                    const float4 t = PJ4[buf * NB4 + c4];
+                    row[q][4 * c4] = t.x; row[q][4 * c4 + 1] = t.y;
+                    row[q][4 * c4 + 2] = t.z; row[q][4 * c4 + 3] = t.w;
+                  }
+                }
+            }
+            if (tid == 0) {
+              const int t = pl[k0 + j];
+              pl[k0 + j] = pl[k0 + p];
+              pl[k0 + p] = t;
+            }
+          }
+          // LAPACK xGETRF2: scale by the reciprocal unless the pivot is subnormal; a zero
+          // pivot leaves the column as it is (its update is then a no-op).
+          const bool nz = pv != 0.f;
+          const bool recip = fabsf(pv) >= 1.17549435e-38f;
+          const float inv = 1.f / pv;
+#pragma unroll
+          for (int q = 0; q < RPT; ++q) {
+            const int r = rbase + T * q;
+            l[q] = 0.f;
+            if (r > j && r < m) {
+              l[q] = row[q][j];
+              if (nz) {
+                l[q] = recip ? l[q] * inv : l[q] / pv;
+                row[q][j] = l[q];
+              }
+            }
+          }
+        } else {
+          if (tid == j) {
+#pragma unroll
+            for (int c4 = 0; c4 < NB4; ++c4)
+              PB4[buf * NB4 + c4] = make_float4(row[0][4 * c4], row[0][4 * c4 + 1],
+                                                row[0][4 * c4 + 2], row[0][4 * c4 + 3]);
+          }
+          __syncthreads();
+          const float d = U[buf * NB + j];
+          const float pp = 1.f - d, pm = 1.f + d;
+          const bool plus = fabsf(pp) >= fabsf(pm);
+          const float sk = plus ? 1.f : -1.f;
+          const float piv = plus ? pp : pm;
+          if (tid == j) my_s = sk;
+#pragma unroll
+          for (int q = 0; q < RPT; ++q) {
+            const int r = rbase + T * q;
+            l[q] = 0.f;
+            if (r > j && r < m) {
+              l[q] = (-sk * row[q][j]) / piv;
+              row[q][j] = l[q];
+            }
+          }
+        }
+        // rank-1 update of the columns right of j (rows outside (j, m) have l = 0)
+#pragma unroll
+        for (int c4 = (j + 1) / 4; c4 < NB4; ++c4) {
+          const float4 pc = PB4[buf * NB4 + c4];
+          const float pcv[4] = {pc.x, pc.y, pc.z, pc.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int c = 4 * c4 + e;
+            if (c > j) {
+#pragma unroll
+              for (int q = 0; q < RPT; ++q) row[q][c] -= l[q] * pcv[e];
+            }
+          }
+        }
+        buf ^= 1;
+      }
+    });
+
+    // ---- registers -> LDS panel
+#pragma unroll
+    for (int q = 0; q < RPT; ++q) {
+      const int r = tid + T * q;
+      if (r < m) {
+#pragma unroll
+        for (int c = 0; c < NB; ++c) P[sw(r, c)] = row[q][c];
+      }
+    }
+    if (!PIVOT && tid < kb) a.s[(int64_t)b * n + k0 + tid] = my_s;
+    __syncthreads();
 
     if constexpr (!PIVOT) {
       // tau of the panel's columns from the finished multipliers (rows below the diagonal)
-      const int c = tid >> 3, sub = tid & 7;
-      if (c < kb) {
+      for (int c = tid >> 3; c < kb; c += T / 8) {
+        const int sub = tid & 7;
         float acc = 0.f;
         for (int r = c + 1 + sub; r < m; r += 8) {
-          const float y = P[r * ldp + c];
+          const float y = P[sw(r, c)];
           acc += y * y;
         }
         acc = group8_sum(acc);
@@ -158,95 +300,112 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
       }
     }
 
-    // ---- write the factored panel back (same physical rows it came from)
-    for (int idx = tid; idx < m * kb; idx += kLuThreads) {
-      const int r = idx / kb, c = idx - r * kb;
-      const int pr = PIVOT ? pl[k0 + r] : k0 + r;
-      dst[(int64_t)pr * n + k0 + c] = P[r * ldp + c];
-    }
-    if (k1 >= n) break;  // uniform: no trailing matrix (and kb == nb below this line)
-
-    // ---- X = L11^-1 (unit lower): 8 lanes per column, forward substitution down the
-    //      column, into U[i*nb + j]; then copied over L11/U11 in the panel (unit diagonal,
-    //      zeros above) so that rows 0..nb of P hold X for the MFMA below.
-    {
-      const int j = tid >> 3, sub = tid & 7;
-      if (j < nb) {
-        for (int i = j + 1; i < nb; ++i) {
-          float part = 0.f;
-          for (int q = j + sub; q < i; q += 8) {
-            const float xq = (q == j) ? 1.f : U[q * nb + j];
-            part += P[i * ldp + q] * xq;
-          }
-          part = group8_sum(part);
-          if (sub == 0) U[i * nb + j] = -part;
-          wave_lds_order();
+    // ---- factored panel -> HBM (same physical rows it came from)
+    if (a.vec4) {
+      const int tot = m * NB4;
+      for (int f = tid; f < tot; f += T) {
+        const int r = f / NB4, c = 4 * (f - r * NB4);
+        if (c < kb) {
+          const int pr = PIVOT ? pl[k0 + r] : k0 + r;
+          *reinterpret_cast<float4*>(dst + (int64_t)pr * n + k0 + c) =
+              make_float4(P[sw(r, c)], P[sw(r, c + 1)], P[sw(r, c + 2)], P[sw(r, c + 3)]);
         }
       }
+    } else {
+      for (int idx = tid; idx < m * kb; idx += T) {
+        const int r = idx / kb, c = idx - r * kb;
+        const int pr = PIVOT ? pl[k0 + r] : k0 + r;
+        dst[(int64_t)pr * n + k0 + c] = P[sw(r, c)];
+      }
     }
-    __syncthreads();
-    for (int idx = tid; idx < nb * nb; idx += kLuThreads) {
-      const int i = idx / nb, c = idx - i * nb;
-      P[i * ldp + c] = (c < i) ? U[i * nb + c] : (c == i ? 1.f : 0.f);
-    }
-    __syncthreads();
+    if (k1 >= n) break;  // uniform: no trailing matrix (and kb == NB below this line)
 
-    // ---- trailing update in chunks of 64 columns
-    for (int c0 = k1; c0 < n; c0 += 64) {
-      // -U12 chunk = -(X * A12[:, c0:c0+64]) into U[k][j], waves 0 .. 2*ceil(nb/32)-1
-      const int nqm = (nb + 31) >> 5;
-      if (wid < 2 * nqm) {
-        const int mi = wid >> 1, nj = wid & 1;
-        const int i = mi * 32 + l32;
-        const int col = c0 + nj * 32 + l32;
-        f32x16 acc = zero16();
-        for (int kk = 0; kk < nb; kk += 2) {
-          const int k = kk + h;
-          const float av = (i < nb) ? P[i * ldp + k] : 0.f;
-          const int pr = PIVOT ? pl[k0 + k] : k0 + k;
-          const float bv = (col < n) ? cur[(int64_t)pr * n + col] : 0.f;
-          acc = mfma(av, bv, acc);
-        }
+    // ---- X = L11^-1 (unit lower) into panel rows 0..NB: wave w sweeps columns
+    //      w*CPW .. w*CPW+CPW-1, lane i holding row i; x_i -= L[i][k] x_k for i > k >= c.
+    {
+      float Lr[NB];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int ii = mi * 32 + acc_row(r, lane);
-          if (ii < nb) U[ii * 64 + nj * 32 + l32] = -acc[r];
+      for (int k = 0; k < NB; ++k) Lr[k] = (lane < NB && k < lane) ? P[sw(lane, k)] : 0.f;
+      __syncthreads();
+      float x[CPW];
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) x[u] = (lane == wid * CPW + u) ? 1.f : 0.f;
+      static_for<0, NB - 1>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        int ln = lane, c0w = __builtin_amdgcn_readfirstlane(wid * CPW);  // laundered: masks stay local
+        asm volatile("" : "+v"(ln), "+s"(c0w));
+#pragma unroll
+        for (int u = 0; u < CPW; ++u) {
+          const float xk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[u]), k));
+          if (k >= c0w + u && ln > k) x[u] -= Lr[k] * xk;
+        }
+      });
+      if (lane < NB) {
+#pragma unroll
+        for (int u = 0; u < CPW; ++u) P[sw(lane, wid * CPW + u)] = x[u];
+      }
+      __syncthreads();
+    }
+
+    // ---- trailing update, 64 columns at a time
+    for (int c0 = k1; c0 < n; c0 += 64) {
+      // -U12 = -(X A12[:, c0:c0+64]) as (NB/16) x 4 blocks of 16x16 spread over the waves
+      {
+        constexpr int NBI = NB / 16, NJOB = NBI * 4;
+        for (int job = wid; job < NJOB; job += NW) {
+          const int bi = job >> 2, bj = job & 3;
+          const int col = c0 + bj * 16 + l16;
+          float bv[NB4];
+#pragma unroll
+          for (int t = 0; t < NB4; ++t) {
+            const int k = 4 * t + q4;
+            const int pr = PIVOT ? pl[k0 + k] : k0 + k;
+            bv[t] = (col < n) ? cur[(int64_t)pr * n + col] : 0.f;
+          }
+          const int i = bi * 16 + l16;
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < NB4; ++t) acc = mfma16(P[sw(i, 4 * t + q4)], bv[t], acc);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) U[(bi * 16 + 4 * q4 + r) * 64 + bj * 16 + l16] = -acc[r];
         }
       }
       __syncthreads();
 
-      // A22[:, chunk] += L21 * (-U12): one 32-row tile per wave at a time
+      // A22[:, chunk] += L21 (-U12): one 32-row tile per wave at a time
       const int ntr = (n - k1 + 31) >> 5;
-      for (int tr = wid; tr < ntr; tr += kLuThreads / 64) {
+      for (int tr = wid; tr < ntr; tr += NW) {
         const int r0 = k1 + tr * 32;
-        f32x16 acc[2];
+        f32x16 c[2];
 #pragma unroll
         for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int row = r0 + acc_row(r, lane), col = c0 + nj * 32 + l32;
+            const int rw = r0 + acc_row(r, lane), col = c0 + nj * 32 + l32;
             float v = 0.f;
-            if (row < n && col < n) {
-              const int pr = PIVOT ? pl[row] : row;
+            if (rw < n && col < n) {
+              const int pr = PIVOT ? pl[rw] : rw;
               v = cur[(int64_t)pr * n + col];
             }
-            acc[nj][r] = v;
+            c[nj][r] = v;
           }
         const int lr = r0 - k0 + l32;
-        for (int kk = 0; kk < nb; kk += 2) {
+        const bool in = lr < m;
+#pragma unroll
+        for (int kk = 0; kk < NB; kk += 2) {
           const int k = kk + h;
-          const float av = (lr < m) ? P[lr * ldp + k] : 0.f;
-          acc[0] = mfma(av, U[k * 64 + l32], acc[0]);
-          acc[1] = mfma(av, U[k * 64 + 32 + l32], acc[1]);
+          const float av = in ? P[sw(lr, k)] : 0.f;
+          c[0] = mfma(av, U[k * 64 + l32], c[0]);
+          c[1] = mfma(av, U[k * 64 + 32 + l32], c[1]);
         }
 #pragma unroll
         for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int row = r0 + acc_row(r, lane), col = c0 + nj * 32 + l32;
-            if (row < n && col < n) {
-              const int pr = PIVOT ? pl[row] : row;
-              dst[(int64_t)pr * n + col] = acc[nj][r];
+            const int rw = r0 + acc_row(r, lane), col = c0 + nj * 32 + l32;
+            if (rw < n && col < n) {
+              const int pr = PIVOT ? pl[rw] : rw;
+              dst[(int64_t)pr * n + col] = c[nj][r];
             }
           }
       }
@@ -256,11 +415,13 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
   __syncthreads();
 
   if constexpr (PIVOT) {
-    for (int i = tid; i < n; i += kLuThreads) a.perm[(int64_t)b * n + i] = pl[i];
-    float* L = a.L + b * a.sl;
-    for (int idx = tid; idx < n * n; idx += kLuThreads) {
-      const int i = idx / n, j = idx - i * n;
-      L[idx] = (j < i) ? dst[(int64_t)pl[i] * n + j] : (j == i ? 1.f : 0.f);
+    for (int i = tid; i < n; i += T) a.perm[(int64_t)b * n + i] = pl[i];
+    if (a.L) {
+      float* L = a.L + b * a.sl;
+      for (int idx = tid; idx < n * n; idx += T) {
+        const int i = idx / n, j = idx - i * n;
+        L[idx] = (j < i) ? dst[(int64_t)pl[i] * n + j] : (j == i ? 1.f : 0.f);
+      }
     }
   }
 }

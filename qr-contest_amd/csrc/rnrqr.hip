@@ -78,12 +78,6 @@ int check_common(int64_t batch, int64_t n) {
   return RNR_OK;
 }
 
-int lu_panel_width(int n) {
-  for (int nb = 64; nb >= 8; nb >>= 1)
-    if (lu_lds_bytes(n, nb) <= kLdsMax) return nb;
-  return 0;
-}
-
 int hip_status() { return hipGetLastError() == hipSuccess ? RNR_OK : RNR_ERR_HIP; }
 
 template <typename K>
@@ -95,30 +89,41 @@ int set_lds(K kernel, size_t bytes) {
              : RNR_ERR_HIP;
 }
 
+template <bool PIVOT, int NB, int RPT>
+int launch_lu_nb(const LuArgs& a, int64_t batch, hipStream_t st) {
+  const size_t lds = lu_lds_bytes(a.n, NB);
+  if (lds > kLdsMax) return RNR_ERR_UNSUPPORTED_N;
+  if (int e = set_lds(k_lu<PIVOT, NB, RPT>, lds)) return e;
+  k_lu<PIVOT, NB, RPT><<<dim3((unsigned)batch), dim3(kLuThreads), lds, st>>>(a);
+  return hip_status();
+}
+
 int launch_lu(bool pivot, const float* src, int64_t ss, float* dst, int64_t sd, int64_t batch,
               int n, int* perm, float* L, float* s, float* tau, hipStream_t st) {
   LuArgs a;
-  a.src = src; a.ss = ss; a.dst = dst; a.sd = sd; a.n = n; a.nb = lu_panel_width(n);
+  a.src = src; a.ss = ss; a.dst = dst; a.sd = sd; a.n = n;
+  a.vec4 = (n % 4 == 0) && (ss % 4 == 0) && (sd % 4 == 0) && aligned(src, 16) && aligned(dst, 16);
   a.perm = perm; a.L = L; a.sl = (int64_t)n * n; a.s = s; a.tau = tau;
-  if (a.nb == 0) return RNR_ERR_UNSUPPORTED_N;
-  const size_t lds = lu_lds_bytes(n, a.nb);
+  const int nb = lu_panel_nb(n);
+  // rows per thread: n <= kLuThreads * RPT
   if (pivot) {
-    if (int e = set_lds(k_lu<true>, lds)) return e;
-    k_lu<true><<<dim3((unsigned)batch), dim3(kLuThreads), lds, st>>>(a);
-  } else {
-    if (int e = set_lds(k_lu<false>, lds)) return e;
-    k_lu<false><<<dim3((unsigned)batch), dim3(kLuThreads), lds, st>>>(a);
+    if (nb == 64) return launch_lu_nb<true, 64, 1>(a, batch, st);
+    if (nb == 32) return launch_lu_nb<true, 32, 2>(a, batch, st);
+    return launch_lu_nb<true, 16, 4>(a, batch, st);
   }
-  return hip_status();
+  if (nb == 64) return launch_lu_nb<false, 64, 1>(a, batch, st);
+  if (nb == 32) return launch_lu_nb<false, 32, 2>(a, batch, st);
+  return launch_lu_nb<false, 16, 4>(a, batch, st);
 }
 
 // C[b] upper tiles of X^T Y (see gemm_tn.hpp); closure = masked + row-scaled.
 int launch_tn(bool closure, const float* X, int64_t sx, const float* Y, int64_t sy, float* C,
-              int64_t sc, const float* rs, int64_t batch, int n, bool klo_from_j, hipStream_t st) {
+              int64_t sc, const float* rs, const int* lperm, int64_t batch, int n, bool klo_from_j,
+              hipStream_t st) {
   const bool big = n > 256;
   const int BM = big ? 128 : 64;
   TnArgs a;
-  a.X = X; a.sx = sx; a.Y = Y; a.sy = sy; a.C = C; a.sc = sc; a.rs = rs; a.n = n;
+  a.X = X; a.sx = sx; a.Y = Y; a.sy = sy; a.C = C; a.sc = sc; a.rs = rs; a.lperm = lperm; a.n = n;
   a.nt = (n + BM - 1) / BM;
   a.ntiles = a.nt * (a.nt + 1) / 2;
   a.klo_from_j = klo_from_j ? 1 : 0;
@@ -150,12 +155,12 @@ int launch_chol(float* G, int64_t sg, float* Dinv, int* info, int64_t batch, int
   return hip_status();
 }
 
-int launch_trsm(const float* M, int64_t sm, const float* R, int64_t sr, const float* Dinv, float* Q,
-                int64_t sq, float* Q2, int64_t sq2, const int* perm, int64_t batch, int n,
-                hipStream_t st) {
+int launch_trsm(const float* M, int64_t sm, const int* mperm, const float* R, int64_t sr,
+                const float* Dinv, float* Q, int64_t sq, float* Q2, int64_t sq2, const int* perm,
+                int64_t batch, int n, hipStream_t st) {
   TrsmArgs a;
   a.M = M; a.sm = sm; a.R = R; a.sr = sr; a.Dinv = Dinv; a.Q = Q; a.sq = sq; a.Q2 = Q2; a.sq2 = sq2;
-  a.perm = perm; a.n = n; a.nrb = (n + 63) / 64;
+  a.perm = perm; a.mperm = mperm; a.n = n; a.nrb = (n + 63) / 64;
   const int64_t total = batch * a.nrb;
   if (total > INT32_MAX) return RNR_ERR_INVALID_ARG;
   a.total = (int)total;
@@ -167,24 +172,27 @@ int launch_trsm(const float* M, int64_t sm, const float* R, int64_t sr, const fl
   return hip_status();
 }
 
-// One CholeskyQR pass: Q = M chol(M^T M + mu I)^-1, R left in G.
-int cholqr_pass(const float* M, int64_t sm, bool m_unit_lower, float* G, float* Dinv, int* info,
+// One CholeskyQR pass: Q = M chol(M^T M + mu I)^-1, R left in G.  With lperm, M is the unit-
+// lower L held in A's row order (the LU's in-place factor) and is read through lperm.
+int cholqr_pass(const float* M, int64_t sm, const int* lperm, float* G, float* Dinv, int* info,
                 bool keep_info, float* Q, float* Q2, const int* perm, int64_t batch, int n,
                 hipStream_t st) {
   const int64_t nn = (int64_t)n * n;
-  if (int e = launch_tn(false, M, sm, M, sm, G, nn, nullptr, batch, n, m_unit_lower, st)) return e;
+  if (int e = launch_tn(false, M, sm, M, sm, G, nn, nullptr, lperm, batch, n, lperm != nullptr, st))
+    return e;
   if (int e = launch_chol(G, nn, Dinv, info, batch, n, keep_info, st)) return e;
-  return launch_trsm(M, sm, G, nn, Dinv, Q, nn, Q2, nn, perm, batch, n, st);
+  return launch_trsm(M, sm, lperm, G, nn, Dinv, Q, nn, Q2, nn, perm, batch, n, st);
 }
 
-// The frame: LU of A into ws.W / ws.L / ws.perm, CholeskyQR2 of L, Q = P Q2 -> Q (and Q2).
+// The frame: LU of A in place into ws.W (+ ws.perm), CholeskyQR2 of L read through perm,
+// Q = P Q2 -> Q (and Qcopy).  Q1 goes to ws.L.
 int frame(const float* A, int64_t sa, const Ws& w, float* Q, float* Qcopy, int* info, int64_t batch,
           int n, hipStream_t st) {
   const int64_t nn = (int64_t)n * n;
-  if (int e = launch_lu(true, A, sa, w.W, nn, batch, n, w.perm, w.L, nullptr, nullptr, st)) return e;
-  if (int e = cholqr_pass(w.L, nn, true, w.G, w.Dinv, info, false, w.W, nullptr, nullptr, batch, n, st))
+  if (int e = launch_lu(true, A, sa, w.W, nn, batch, n, w.perm, nullptr, nullptr, nullptr, st)) return e;
+  if (int e = cholqr_pass(w.W, nn, w.perm, w.G, w.Dinv, info, false, w.L, nullptr, nullptr, batch, n, st))
     return e;
-  return cholqr_pass(w.W, nn, false, w.G, w.Dinv, info, true, Q, Qcopy, w.perm, batch, n, st);
+  return cholqr_pass(w.L, nn, nullptr, w.G, w.Dinv, info, true, Q, Qcopy, w.perm, batch, n, st);
 }
 
 int check_ws(void* ws, size_t ws_bytes, size_t need) {
@@ -235,7 +243,7 @@ int rnr_qr_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride, f
   int* inf = info ? info : w.info;
   if (int e = frame(A, batch_stride, w, w.Qb, H, inf, batch, ni, st)) return e;
   if (int e = launch_lu(false, H, nn, H, nn, batch, ni, nullptr, nullptr, w.s, tau, st)) return e;
-  return launch_tn(true, w.Qb, nn, A, batch_stride, H, nn, w.s, batch, ni, false, st);
+  return launch_tn(true, w.Qb, nn, A, batch_stride, H, nn, w.s, nullptr, batch, ni, false, st);
 }
 
 int rnr_lu_f32_workspace(int64_t batch, int64_t n, size_t* bytes) {
@@ -277,7 +285,7 @@ int rnr_cholqr_f32(const float* M, int64_t batch, int64_t n, int64_t batch_strid
   Ws w;
   carve(batch, n, kCholqrNeed, static_cast<char*>(ws), &w);
   float* G = R ? R : w.G;
-  return cholqr_pass(M, batch_stride, false, G, w.Dinv, info ? info : w.info, false, Q, nullptr,
+  return cholqr_pass(M, batch_stride, nullptr, G, w.Dinv, info ? info : w.info, false, Q, nullptr,
                      nullptr, batch, (int)n, reinterpret_cast<hipStream_t>(stream));
 }
 

@@ -26,6 +26,8 @@ struct TrsmArgs {
   float* Q2;          // optional copy (nullptr: none), batch stride sq2
   int64_t sq2;
   const int* perm;    // optional row scatter [batch][n] (nullptr: identity)
+  const int* mperm;   // non-null: M is the unit-lower L stored in A's row order (the LU's
+                      // in-place factor); logical row r is physical row mperm[b][r]
   int n, nrb, total;
 };
 
@@ -106,7 +108,11 @@ __global__ __launch_bounds__(256) void k_trsm(TrsmArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = r0 + mi * 32 + acc_row(r, lane), col = c0 + nj * 32 + l32;
-      acc[r] = (row < n && col < n) ? M[(int64_t)row * n + col] : 0.f;
+      if (a.mperm)
+        acc[r] = (row < n && col < row) ? M[(int64_t)a.mperm[(int64_t)b * n + row] * n + col]
+                                        : (row < n && col == row ? 1.f : 0.f);
+      else
+        acc[r] = (row < n && col < n) ? M[(int64_t)row * n + col] : 0.f;
     }
     if (c0 > 0) {
       int buf = 0;

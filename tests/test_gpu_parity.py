@@ -221,7 +221,12 @@ def test_stage_lu_matches_getrf(rnr, wl, n):
     perm, L = perm.cpu(), L.cpu()
     pref, Lref = orc.lu_factor(A)
     assert torch.equal(perm, pref), "pivot order differs from getrf (first-max rule)"
-    assert (L - Lref).abs().max().item() < 1e-4
+    # both fp32 factors against the fp64 one (same pivots): ours within 4x LAPACK's error
+    p64, L64 = orc.lu_factor(A.double())
+    assert torch.equal(p64, pref)
+    e_ref = (Lref.double() - L64).abs().max().item()
+    e_hip = (L.double() - L64).abs().max().item()
+    assert e_hip <= 4 * e_ref + 1e-6, (n, e_hip, e_ref)
     assert torch.equal(torch.triu(L, 1), torch.zeros_like(L))
     assert torch.all(torch.diagonal(L, dim1=-2, dim2=-1) == 1.0)
     assert L.abs().max().item() <= 1.0
