@@ -10,6 +10,7 @@ classes cycled (synthetic, seeded).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import importlib
 import json
 import os
@@ -38,6 +39,27 @@ def _events_ms(fn, reps: int, stream) -> float:
     stop.record(stream)
     stop.synchronize()
     return start.elapsed_time(stop) / reps
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_headline_256x512.md")
+# bench kernel label -> the kernel symbol in the rocprofv3 counter summary
+PROFILE_SYMBOL = {"k_trsm": "rnr::k_trsm<true>", "k_chol": "rnr::k_chol",
+                  "k_lu<true> (LU)": "rnr::k_lu<true, 64, 1>", "k_lu<false> (chart)": "rnr::k_lu<false, 64, 1>",
+                  "k_tn_upper": "rnr::k_tn_upper<128, false, false, true>"}
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH/WRITE summary
+    (headline workload only), or None."""
+    sym = PROFILE_SYMBOL.get(kernel)
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic ") and line[len("traffic "):].rsplit(" ", 1)[0] == sym:
+                    return int(line.rsplit(" ", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def _cpu_name() -> str:
@@ -93,6 +115,9 @@ def main() -> None:
     ap.add_argument("--config", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-geqrf", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 256 MiB device copy three times (the known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -109,6 +134,14 @@ def main() -> None:
     cfg = wl.CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.copy_calibration:
+        x = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        del x, y
 
     A_cpu = wl.make_batch(args.config)
     A = A_cpu.to(dev)
@@ -129,39 +162,44 @@ def main() -> None:
 
     # validity of what was timed: gates on one matrix per class of the last step's output
     from oracle import checker
-    k = min(cfg.batch, 6)
-    H, tau = plan.H[:k].cpu(), plan.tau[:k].cpu()
-    fr, og, ft, ot, ok = checker.check(A_cpu[:k], H, tau)
+    n_checked = min(cfg.batch, 6)
+    H, tau = plan.H[:n_checked].cpu(), plan.tau[:n_checked].cpu()
+    fr, og, ft, ot, ok = checker.check(A_cpu[:n_checked], H, tau)
     info_ok = int(plan.info.abs().sum().item()) == 0
 
-    # the path's kernels one at a time, through the single-launch stage entry points
-    stages = {}
+    # per-kernel times of the live path: rnr_qr_f32_timed records an event before each launch
     lib = native.lib()
-    Lb = torch.empty_like(A)
-    perm = torch.empty(cfg.batch, cfg.n, dtype=torch.int32, device=dev)
-    ws_lu = torch.empty(native.workspace_bytes("lu", cfg.batch, cfg.n), dtype=torch.uint8, device=dev)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(native.RNR_QR_TIMED_EVENTS)]
+    for e in evs:
+        e.record(stream)  # creates the underlying hipEvent
+    handles = (ctypes.c_void_p * len(evs))(*[e.cuda_event for e in evs])
     nn = cfg.n * cfg.n
-
-    def run_lu():
-        native.check("rnr_lu_f32", lib.rnr_lu_f32(A.data_ptr(), cfg.batch, cfg.n, nn, Lb.data_ptr(),
-                                                  perm.data_ptr(), ws_lu.data_ptr(), ws_lu.numel(),
-                                                  stream.cuda_stream))
-    Yb = plan.H.clone()
-    s_b = torch.empty(cfg.batch, cfg.n, device=dev)
-    t_b = torch.empty(cfg.batch, cfg.n, device=dev)
-
-    def run_chart():
-        native.check("rnr_chart_f32", lib.rnr_chart_f32(Yb.data_ptr(), cfg.batch, cfg.n, s_b.data_ptr(),
-                                                        t_b.data_ptr(), stream.cuda_stream))
-    run_lu(); run_chart()
+    stage_ms = {k: 0.0 for k in native.QR_STAGES}
+    reps = max(3, args.steps)
     torch.cuda.synchronize()
-    reps = max(3, args.steps // 2)
-    stages["k_lu_pivot_ms"] = _events_ms(run_lu, reps, stream)
-    stages["k_lu_chart_ms"] = _events_ms(run_chart, reps, stream)
+    for _ in range(reps):
+        st = lib.rnr_qr_f32_timed(A.data_ptr(), cfg.batch, cfg.n, nn, plan.H.data_ptr(), plan.tau.data_ptr(),
+                                  plan.info.data_ptr(), plan.ws.data_ptr(), plan.ws.numel(), stream.cuda_stream,
+                                  handles, len(evs))
+        native.check("rnr_qr_f32_timed", st)
+        evs[-1].synchronize()
+        for i, k in enumerate(native.QR_STAGES):
+            stage_ms[k] += evs[i].elapsed_time(evs[i + 1]) / reps
 
+    # algorithmic flops per matrix of each launch (minimal counts, not what the kernel executes)
     n3 = float(cfg.n) ** 3
-    lu_flops = 2.0 / 3.0 * n3 * cfg.batch
-    lu_tflops = lu_flops / (stages["k_lu_pivot_ms"] / 1e3) / 1e12
+    flops = {"lu": 2 / 3 * n3, "gram_L": n3 / 3, "chol_1": n3 / 3, "trsm_1": n3, "gram_Q1": n3,
+             "chol_2": n3 / 3, "trsm_2": n3, "chart": 2 / 3 * n3, "closure": n3}
+    kernels = {"k_lu<true> (LU)": ["lu"], "k_lu<false> (chart)": ["chart"], "k_chol": ["chol_1", "chol_2"],
+               "k_trsm": ["trsm_1", "trsm_2"], "k_tn_upper": ["gram_L", "gram_Q1", "closure"]}
+    per_kernel = {}
+    for name, ks in kernels.items():
+        t = sum(stage_ms[k] for k in ks)
+        f = sum(flops[k] for k in ks) * cfg.batch
+        per_kernel[name] = {"ms_per_step": t, "launches": len(ks), "avg_launch_us": 1e3 * t / len(ks),
+                            "tflops": f / (t / 1e3) / 1e12}
+    dom = max(per_kernel, key=lambda k: per_kernel[k]["ms_per_step"])
+    dom_tflops = per_kernel[dom]["tflops"]
 
     gpu_geqrf = None
     if not args.no_geqrf:
@@ -193,12 +231,13 @@ def main() -> None:
         "config": {"workload": cfg.name, "batch": cfg.batch, "n": cfg.n},
         "roofline": {
             "bound": "mfma",
-            "achieved": lu_tflops,
+            "achieved": dom_tflops,
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": lu_tflops / PEAK_FP32_MFMA_TFLOPS,
-            "traffic": None,
-            "kernel": "k_lu<true> (partial-pivot LU, (2/3) n^3 flops per matrix)",
+            "frac": dom_tflops / PEAK_FP32_MFMA_TFLOPS,
+            "traffic": measured_traffic(dom) if args.config == 4 else None,
+            "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if args.config == 4 else None,
+            "kernel": dom,
         },
         "path": {
             "nominal_tflops": nominal_tflops,
@@ -206,9 +245,10 @@ def main() -> None:
             "hbm_gbs_algorithmic": gbs,
             "wall_ms_per_step": wall_ms,
         },
-        "stages_ms": stages,
+        "stages_ms": stage_ms,
+        "kernels": per_kernel,
         "gates": {"factor_max": fr, "factor_gate": ft, "ortho_max": og, "ortho_gate": ot,
-                  "checked": k, "pass": bool(ok.all()) and info_ok},
+                  "checked": n_checked, "pass": bool(ok.all()) and info_ok},
         "gpu_torch_geqrf": gpu_geqrf,
         "cpu_baseline": cpu,
     }

@@ -66,6 +66,16 @@ int rnr_qr_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride,
                float* H, float* tau, int32_t* info,
                void* ws, size_t ws_bytes, rnr_stream_t stream);
 
+/* Same as rnr_qr_f32, and records events[i] (hipEvent_t handles created by the caller) on
+ * the stream before launch i of the sequence and events[9] after the last, for per-kernel
+ * timing of the live path: 0 LU, 1 Gram(L), 2 Cholesky, 3 solve L R^-1, 4 Gram(Q1),
+ * 5 Cholesky, 6 solve Q1 R^-1 with the row gather, 7 chart, 8 closure.  Stands in for the
+ * reference's event timers around its stages (common/bench.py:12-21). */
+#define RNR_QR_TIMED_EVENTS 10
+int rnr_qr_f32_timed(const float* A, int64_t batch, int64_t n, int64_t batch_stride,
+                     float* H, float* tau, int32_t* info, void* ws, size_t ws_bytes,
+                     rnr_stream_t stream, void* const* events, int n_events);
+
 /* ---- stage entry points (the reference's internal stages, for stage-level parity) ---- */
 
 /* Partial-pivot LU (torch.linalg.lu, reflection_no_reflectors.py:66): perm[b][i] is the

@@ -20,6 +20,9 @@ RNR_ERR_WORKSPACE = 3
 RNR_ERR_HIP = 4
 RNR_ERR_MISALIGNED = 5
 RNR_MAX_N = 2048
+RNR_QR_TIMED_EVENTS = 10
+# the launches of rnr_qr_f32 in order (what rnr_qr_f32_timed's events bracket)
+QR_STAGES = ("lu", "gram_L", "chol_1", "trsm_1", "gram_Q1", "chol_2", "trsm_2", "chart", "closure")
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -33,6 +36,8 @@ SIGNATURES = {
     "rnr_version": (ctypes.c_char_p, []),
     "rnr_qr_f32_workspace": (_int, [_i64, _i64, _szp]),
     "rnr_qr_f32": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "rnr_qr_f32_timed": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp,
+                                ctypes.POINTER(ctypes.c_void_p), _int]),
     "rnr_lu_f32_workspace": (_int, [_i64, _i64, _szp]),
     "rnr_lu_f32": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
     "rnr_cholqr_f32_workspace": (_int, [_i64, _i64, _szp]),

@@ -10,6 +10,7 @@
 //   7. k_trsm            Q = P (Q1 R_b^-1) -> Qb and H (row scatter)            (:77,81)
 //   8. k_lu<false>       chart in place on H: tails Y, signs s, tau             (:139-174,192)
 //   9. k_tn_upper        H_upper = diag(s) triu(Q^T A), masked to j >= i         (:186,195)
+// rnr_qr_f32_timed records one caller event before each launch and one after the last.
 #include "../../include/rnrqr.h"
 #include "common.hpp"
 #include "gemm_tn.hpp"
@@ -160,7 +161,7 @@ int launch_trsm(const float* M, int64_t sm, const int* mperm, const float* R, in
                 int64_t batch, int n, hipStream_t st) {
   TrsmArgs a;
   a.M = M; a.sm = sm; a.R = R; a.sr = sr; a.Dinv = Dinv; a.Q = Q; a.sq = sq; a.Q2 = Q2; a.sq2 = sq2;
-  a.perm = perm; a.mperm = mperm; a.n = n; a.nrb = (n + 63) / 64;
+  a.perm = perm; a.mperm = mperm; a.n = n; a.nrb = (n + kTrsmRows - 1) / kTrsmRows;
   const int64_t total = batch * a.nrb;
   if (total > INT32_MAX) return RNR_ERR_INVALID_ARG;
   a.total = (int)total;
@@ -172,34 +173,75 @@ int launch_trsm(const float* M, int64_t sm, const int* mperm, const float* R, in
   return hip_status();
 }
 
+int check_ws(void* ws, size_t ws_bytes, size_t need) {
+  if (need == 0) return RNR_OK;
+  if (!ws || ws_bytes < need) return RNR_ERR_WORKSPACE;
+  if (!aligned(ws, 256)) return RNR_ERR_MISALIGNED;
+  return RNR_OK;
+}
+
+// Optional per-launch timing: events[i] is recorded on the stream before launch i of the
+// sequence and events[last] after it (the hook behind rnr_qr_f32_timed).
+struct Marks {
+  void* const* ev;
+  int n;
+  int next;
+  int mark(hipStream_t st) {
+    if (!ev) return RNR_OK;
+    if (next >= n) return RNR_ERR_INVALID_ARG;
+    return hipEventRecord(static_cast<hipEvent_t>(ev[next++]), st) == hipSuccess ? RNR_OK : RNR_ERR_HIP;
+  }
+};
+
 // One CholeskyQR pass: Q = M chol(M^T M + mu I)^-1, R left in G.  With lperm, M is the unit-
 // lower L held in A's row order (the LU's in-place factor) and is read through lperm.
 int cholqr_pass(const float* M, int64_t sm, const int* lperm, float* G, float* Dinv, int* info,
                 bool keep_info, float* Q, float* Q2, const int* perm, int64_t batch, int n,
-                hipStream_t st) {
+                hipStream_t st, Marks& mk) {
   const int64_t nn = (int64_t)n * n;
+  if (int e = mk.mark(st)) return e;
   if (int e = launch_tn(false, M, sm, M, sm, G, nn, nullptr, lperm, batch, n, lperm != nullptr, st))
     return e;
+  if (int e = mk.mark(st)) return e;
   if (int e = launch_chol(G, nn, Dinv, info, batch, n, keep_info, st)) return e;
+  if (int e = mk.mark(st)) return e;
   return launch_trsm(M, sm, lperm, G, nn, Dinv, Q, nn, Q2, nn, perm, batch, n, st);
 }
 
 // The frame: LU of A in place into ws.W (+ ws.perm), CholeskyQR2 of L read through perm,
 // Q = P Q2 -> Q (and Qcopy).  Q1 goes to ws.L.
 int frame(const float* A, int64_t sa, const Ws& w, float* Q, float* Qcopy, int* info, int64_t batch,
-          int n, hipStream_t st) {
+          int n, hipStream_t st, Marks& mk) {
   const int64_t nn = (int64_t)n * n;
+  if (int e = mk.mark(st)) return e;
   if (int e = launch_lu(true, A, sa, w.W, nn, batch, n, w.perm, nullptr, nullptr, nullptr, st)) return e;
-  if (int e = cholqr_pass(w.W, nn, w.perm, w.G, w.Dinv, info, false, w.L, nullptr, nullptr, batch, n, st))
+  if (int e = cholqr_pass(w.W, nn, w.perm, w.G, w.Dinv, info, false, w.L, nullptr, nullptr, batch, n,
+                          st, mk))
     return e;
-  return cholqr_pass(w.L, nn, nullptr, w.G, w.Dinv, info, true, Q, Qcopy, w.perm, batch, n, st);
+  return cholqr_pass(w.L, nn, nullptr, w.G, w.Dinv, info, true, Q, Qcopy, w.perm, batch, n, st, mk);
 }
 
-int check_ws(void* ws, size_t ws_bytes, size_t need) {
-  if (need == 0) return RNR_OK;
-  if (!ws || ws_bytes < need) return RNR_ERR_WORKSPACE;
-  if (!aligned(ws, 256)) return RNR_ERR_MISALIGNED;
-  return RNR_OK;
+// The whole path (see the launch list at the top of this file).
+int qr_path(const float* A, int64_t batch, int64_t n, int64_t batch_stride, float* H, float* tau,
+            int32_t* info, void* ws, size_t ws_bytes, hipStream_t st, Marks& mk) {
+  if (int e = check_common(batch, n)) return e;
+  if (batch == 0) return RNR_OK;
+  if (!A || !H || !tau || batch_stride < n * n) return RNR_ERR_INVALID_ARG;
+  if (!aligned(A, 4) || !aligned(H, 4) || !aligned(tau, 4)) return RNR_ERR_MISALIGNED;
+  const size_t need = carve(batch, n, kQrNeed, nullptr, nullptr);
+  if (int e = check_ws(ws, ws_bytes, need)) return e;
+  Ws w;
+  carve(batch, n, kQrNeed, static_cast<char*>(ws), &w);
+  const int ni = (int)n;
+  const int64_t nn = n * n;
+  int* inf = info ? info : w.info;
+  if (int e = frame(A, batch_stride, w, w.Qb, H, inf, batch, ni, st, mk)) return e;
+  if (int e = mk.mark(st)) return e;
+  if (int e = launch_lu(false, H, nn, H, nn, batch, ni, nullptr, nullptr, w.s, tau, st)) return e;
+  if (int e = mk.mark(st)) return e;
+  if (int e = launch_tn(true, w.Qb, nn, A, batch_stride, H, nn, w.s, nullptr, batch, ni, false, st))
+    return e;
+  return mk.mark(st);
 }
 
 }  // namespace
@@ -229,21 +271,20 @@ int rnr_qr_f32_workspace(int64_t batch, int64_t n, size_t* bytes) {
 
 int rnr_qr_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride, float* H, float* tau,
                int32_t* info, void* ws, size_t ws_bytes, rnr_stream_t stream) {
-  if (int e = check_common(batch, n)) return e;
-  if (batch == 0) return RNR_OK;
-  if (!A || !H || !tau || batch_stride < n * n) return RNR_ERR_INVALID_ARG;
-  if (!aligned(A, 4) || !aligned(H, 4) || !aligned(tau, 4)) return RNR_ERR_MISALIGNED;
-  const size_t need = carve(batch, n, kQrNeed, nullptr, nullptr);
-  if (int e = check_ws(ws, ws_bytes, need)) return e;
-  Ws w;
-  carve(batch, n, kQrNeed, static_cast<char*>(ws), &w);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int ni = (int)n;
-  const int64_t nn = n * n;
-  int* inf = info ? info : w.info;
-  if (int e = frame(A, batch_stride, w, w.Qb, H, inf, batch, ni, st)) return e;
-  if (int e = launch_lu(false, H, nn, H, nn, batch, ni, nullptr, nullptr, w.s, tau, st)) return e;
-  return launch_tn(true, w.Qb, nn, A, batch_stride, H, nn, w.s, nullptr, batch, ni, false, st);
+  Marks mk{nullptr, 0, 0};
+  return qr_path(A, batch, n, batch_stride, H, tau, info, ws, ws_bytes,
+                 reinterpret_cast<hipStream_t>(stream), mk);
+}
+
+int rnr_qr_f32_timed(const float* A, int64_t batch, int64_t n, int64_t batch_stride, float* H,
+                     float* tau, int32_t* info, void* ws, size_t ws_bytes, rnr_stream_t stream,
+                     void* const* events, int n_events) {
+  if (!events || n_events < RNR_QR_TIMED_EVENTS) return RNR_ERR_INVALID_ARG;
+  for (int i = 0; i < RNR_QR_TIMED_EVENTS; ++i)
+    if (!events[i]) return RNR_ERR_INVALID_ARG;
+  Marks mk{events, n_events, 0};
+  return qr_path(A, batch, n, batch_stride, H, tau, info, ws, ws_bytes,
+                 reinterpret_cast<hipStream_t>(stream), mk);
 }
 
 int rnr_lu_f32_workspace(int64_t batch, int64_t n, size_t* bytes) {
@@ -285,8 +326,9 @@ int rnr_cholqr_f32(const float* M, int64_t batch, int64_t n, int64_t batch_strid
   Ws w;
   carve(batch, n, kCholqrNeed, static_cast<char*>(ws), &w);
   float* G = R ? R : w.G;
+  Marks mk{nullptr, 0, 0};
   return cholqr_pass(M, batch_stride, nullptr, G, w.Dinv, info ? info : w.info, false, Q, nullptr,
-                     nullptr, batch, (int)n, reinterpret_cast<hipStream_t>(stream));
+                     nullptr, batch, (int)n, reinterpret_cast<hipStream_t>(stream), mk);
 }
 
 int rnr_frame_f32_workspace(int64_t batch, int64_t n, size_t* bytes) {
@@ -306,8 +348,9 @@ int rnr_frame_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride
   if (int e = check_ws(ws, ws_bytes, need)) return e;
   Ws w;
   carve(batch, n, kFrameNeed, static_cast<char*>(ws), &w);
+  Marks mk{nullptr, 0, 0};
   return frame(A, batch_stride, w, Q, nullptr, info ? info : w.info, batch, (int)n,
-               reinterpret_cast<hipStream_t>(stream));
+               reinterpret_cast<hipStream_t>(stream), mk);
 }
 
 int rnr_chart_f32(float* Y, int64_t batch, int64_t n, float* s, float* tau, rnr_stream_t stream) {
