@@ -53,7 +53,9 @@ const char* rnr_status_string(int status);
 const char* rnr_version(void);
 
 /* ---- whole path: custom_kernel (reflection_no_reflectors.py:181-196) ------------------
- * Bytes of device workspace rnr_qr_f32 needs for (batch, n).  0 for batch == 0. */
+ * Bytes of device workspace rnr_qr_f32 needs for (batch, n).  0 for batch == 0, and 0 for
+ * n <= 64, where the whole path is one fused launch with everything on chip (ws may then
+ * be NULL). */
 int rnr_qr_f32_workspace(int64_t batch, int64_t n, size_t* bytes);
 
 /* H (batch x n x n, contiguous) and tau (batch x n, contiguous) from A.
@@ -69,7 +71,8 @@ int rnr_qr_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride,
 /* Same as rnr_qr_f32, and records events[i] (hipEvent_t handles created by the caller) on
  * the stream before launch i of the sequence and events[9] after the last, for per-kernel
  * timing of the live path: 0 LU, 1 Gram(L), 2 Cholesky, 3 solve L R^-1, 4 Gram(Q1),
- * 5 Cholesky, 6 solve Q1 R^-1 with the row gather, 7 chart, 8 closure.  Stands in for the
+ * 5 Cholesky, 6 solve Q1 R^-1 with the row gather, 7 chart, 8 closure.  For n <= 64 the
+ * path is one launch: events[0] before it and events[1..9] after it.  Stands in for the
  * reference's event timers around its stages (common/bench.py:12-21). */
 #define RNR_QR_TIMED_EVENTS 10
 int rnr_qr_f32_timed(const float* A, int64_t batch, int64_t n, int64_t batch_stride,

@@ -11,12 +11,20 @@
 //   8. k_lu<false>       chart in place on H: tails Y, signs s, tau             (:139-174,192)
 //   9. k_tn_upper        H_upper = diag(s) triu(Q^T A), masked to j >= i         (:186,195)
 // rnr_qr_f32_timed records one caller event before each launch and one after the last.
+//
+// For n <= kSmallMaxN (64) the whole path is instead one launch of k_small (small.hpp), one
+// matrix per group of lanes of a wave; it needs no workspace.
 #include "../../include/rnrqr.h"
 #include "common.hpp"
 #include "gemm_tn.hpp"
 #include "lu.hpp"
 #include "chol.hpp"
 #include "trsm.hpp"
+#include "small.hpp"
+
+namespace rnr {
+int launch_small(const SmallArgs& a, hipStream_t st);  // small.hip
+}
 
 using namespace rnr;
 
@@ -191,7 +199,15 @@ struct Marks {
     if (next >= n) return RNR_ERR_INVALID_ARG;
     return hipEventRecord(static_cast<hipEvent_t>(ev[next++]), st) == hipSuccess ? RNR_OK : RNR_ERR_HIP;
   }
+  // records every event not yet recorded (a path with fewer launches than stages)
+  int rest(hipStream_t st) {
+    while (ev && next < RNR_QR_TIMED_EVENTS)
+      if (int e = mark(st)) return e;
+    return RNR_OK;
+  }
 };
+
+bool small_path(int64_t n) { return n <= kSmallMaxN; }
 
 // One CholeskyQR pass: Q = M chol(M^T M + mu I)^-1, R left in G.  With lperm, M is the unit-
 // lower L held in A's row order (the LU's in-place factor) and is read through lperm.
@@ -228,6 +244,16 @@ int qr_path(const float* A, int64_t batch, int64_t n, int64_t batch_stride, floa
   if (batch == 0) return RNR_OK;
   if (!A || !H || !tau || batch_stride < n * n) return RNR_ERR_INVALID_ARG;
   if (!aligned(A, 4) || !aligned(H, 4) || !aligned(tau, 4)) return RNR_ERR_MISALIGNED;
+  if (small_path(n)) {
+    if (batch > INT32_MAX) return RNR_ERR_INVALID_ARG;
+    SmallArgs sa;
+    sa.A = A; sa.sa = batch_stride; sa.H = H; sa.tau = tau; sa.info = info;
+    sa.n = (int)n; sa.batch = (int)batch;
+    sa.vec4 = (n % 4 == 0) && (batch_stride % 4 == 0) && aligned(A, 16) && aligned(H, 16);
+    if (int e = mk.mark(st)) return e;
+    if (launch_small(sa, st)) return RNR_ERR_HIP;
+    return mk.rest(st);
+  }
   const size_t need = carve(batch, n, kQrNeed, nullptr, nullptr);
   if (int e = check_ws(ws, ws_bytes, need)) return e;
   Ws w;
@@ -265,7 +291,7 @@ const char* rnr_version(void) { return "0.1.0"; }
 int rnr_qr_f32_workspace(int64_t batch, int64_t n, size_t* bytes) {
   if (!bytes) return RNR_ERR_INVALID_ARG;
   if (int e = check_common(batch, n)) return e;
-  *bytes = batch == 0 ? 0 : carve(batch, n, kQrNeed, nullptr, nullptr);
+  *bytes = (batch == 0 || small_path(n)) ? 0 : carve(batch, n, kQrNeed, nullptr, nullptr);
   return RNR_OK;
 }
 

@@ -54,12 +54,16 @@ def test_status_strings(lib, native):
 
 
 def test_workspace_queries(native, lib):
-    assert native.workspace_bytes("qr", 0, 64) == 0
-    a = native.workspace_bytes("qr", 4, 64)
-    b = native.workspace_bytes("qr", 8, 64)
+    assert native.workspace_bytes("qr", 0, 96) == 0
+    a = native.workspace_bytes("qr", 4, 96)
+    b = native.workspace_bytes("qr", 8, 96)
     assert 0 < a < b
     # four n*n float buffers per matrix at least
-    assert a >= 4 * 4 * 64 * 64 * 4
+    assert a >= 4 * 4 * 96 * 96 * 4
+    # n <= 64 runs the fused one-launch kernel, which needs no workspace
+    for n in (1, 16, 33, 64):
+        assert native.workspace_bytes("qr", 4, n) == 0
+    assert native.workspace_bytes("qr", 4, 65) > 0
     for kind in ("lu", "cholqr", "frame"):
         assert native.workspace_bytes(kind, 3, 100) > 0
     out = ctypes.c_size_t(0)
@@ -72,16 +76,21 @@ def test_workspace_queries(native, lib):
 def test_argument_validation_before_any_launch(native, lib):
     """Every call here must return an error without touching the device."""
     fake = 1 << 20  # never dereferenced: validation fails first
-    need = native.workspace_bytes("qr", 2, 16)
+    n, nn = 80, 80 * 80  # the blocked path (n > 64), which takes a workspace
+    need = native.workspace_bytes("qr", 2, n)
     f = lib.rnr_qr_f32
-    assert f(None, 2, 16, 256, fake, fake, None, fake, need, None) == native.RNR_ERR_INVALID_ARG
-    assert f(fake, 2, 16, 255, fake, fake, None, fake, need, None) == native.RNR_ERR_INVALID_ARG
-    assert f(fake, 2, 0, 256, fake, fake, None, fake, need, None) == native.RNR_ERR_UNSUPPORTED_N
+    assert f(None, 2, n, nn, fake, fake, None, fake, need, None) == native.RNR_ERR_INVALID_ARG
+    assert f(fake, 2, n, nn - 1, fake, fake, None, fake, need, None) == native.RNR_ERR_INVALID_ARG
+    assert f(fake, 2, 0, nn, fake, fake, None, fake, need, None) == native.RNR_ERR_UNSUPPORTED_N
     assert f(fake, 2, 4096, 4096 ** 2, fake, fake, None, fake, need, None) == native.RNR_ERR_UNSUPPORTED_N
-    assert f(fake, 2, 16, 256, fake, fake, None, fake, need - 1, None) == native.RNR_ERR_WORKSPACE
-    assert f(fake, 2, 16, 256, fake, fake, None, None, need, None) == native.RNR_ERR_WORKSPACE
-    assert f(fake, 2, 16, 256, fake, fake, None, fake + 4, need, None) == native.RNR_ERR_MISALIGNED
-    assert f(fake + 2, 2, 16, 256, fake, fake, None, fake, need, None) == native.RNR_ERR_MISALIGNED
+    assert f(fake, 2, n, nn, fake, fake, None, fake, need - 1, None) == native.RNR_ERR_WORKSPACE
+    assert f(fake, 2, n, nn, fake, fake, None, None, need, None) == native.RNR_ERR_WORKSPACE
+    assert f(fake, 2, n, nn, fake, fake, None, fake + 4, need, None) == native.RNR_ERR_MISALIGNED
+    assert f(fake + 2, 2, n, nn, fake, fake, None, fake, need, None) == native.RNR_ERR_MISALIGNED
+    # the fused small-n path validates the same arguments before it launches
+    assert f(None, 2, 16, 256, fake, fake, None, None, 0, None) == native.RNR_ERR_INVALID_ARG
+    assert f(fake, 2, 16, 255, fake, fake, None, None, 0, None) == native.RNR_ERR_INVALID_ARG
+    assert f(fake, 2, 16, 256, fake + 2, fake, None, None, 0, None) == native.RNR_ERR_MISALIGNED
     # batch 0 is a no-op that succeeds with null pointers
     assert f(None, 0, 16, 256, None, None, None, None, 0, None) == native.RNR_OK
     assert lib.rnr_chart_f32(None, 2, 8, fake, fake, None) == native.RNR_ERR_INVALID_ARG
