@@ -2,15 +2,18 @@
 //
 //   mu = 1e-7 * mean(diag G);  G += mu I;  G = R^T R        -- reflection_no_reflectors.py:74-76
 //
-// Blocked right-looking with 64-column blocks.  For block k:
-//   * wave 0 factors the diagonal block with one symmetric row per lane in registers and
-//     the scaled pivot row broadcast through LDS inside the wave (no barriers or fences);
-//   * every wave then forms 8 columns of Dinv_kk = R_kk^-1 by back substitution, one row
-//     per lane in registers, readlane broadcasts; Dinv_kk^T is staged in LDS;
-//   * the block row R_k,> = Dinv_kk^T G_k,> and the trailing update G_>,> -= R_k,>^T R_k,>
-//     (upper 64x64 tiles only) run on MFMA, each wave owning whole output tiles.  When the
-//     block row fits it is also kept in LDS for the trailing update (n <= 576), otherwise
-//     it is read back from G.
+// Blocked right-looking with 64-column blocks and a look-ahead of one diagonal block.  For
+// block k:
+//   * R_kk and Dinv_kk = R_kk^-1 (already in LDS) go to HBM;
+//   * all waves form the block row R_k,> = Dinv_kk^T G_k,> on MFMA, each wave owning whole
+//     32-column strips; when it fits it is also kept in LDS for the trailing update
+//     (n <= 576), otherwise it is read back from G;
+//   * the trailing update G_>,> -= R_k,>^T R_k,> (upper 64x64 tiles, MFMA) is split: wave 0
+//     takes the first diagonal tile -- the next diagonal block -- keeps it in LDS, factors it
+//     (one symmetric row per lane in registers, the scaled pivot row broadcast through LDS
+//     inside the wave, no barriers) and forms its inverse (lane i computes row i of R^-1 by
+//     forward substitution over LDS broadcasts of R's columns), while waves 1..7 update the
+//     other tiles.  The sequential diagonal work thus runs under the trailing update.
 // The diagonal-block inverses go to Dinv ([n][64] per matrix) for the triangular solve
 // that follows.  info records the first column whose pivot was not positive (1-based; NaN
 // counts as not positive).
@@ -34,15 +37,115 @@ constexpr int kCholNb = 64;
 
 inline size_t chol_lds_bytes(int n, bool strip) {
   const size_t w = n > kCholNb ? (size_t)(n - kCholNb) : 1;
-  return sizeof(float) * (2 * 64 * 65 + 64 + 32 + (strip ? 64 * w : 0));
+  return sizeof(float) * (64 * 65 + 64 * 68 + 64 + 64 + 32 + (strip ? 64 * w : 0));
+}
+
+// Wave 0: factor the 64x64 diagonal block held in D (symmetric; the upper part is read) in
+// place into R (upper, zeros below), with R also written column-major into RT (RT[c][k] =
+// R[k][c], row stride 68) and 1 / R[j][j] into RI; returns the first non-positive pivot
+// (column index, or INT_MAX).  Lane i holds symmetric row i of the block in four named
+// 16-wide vectors (compile-time element access keeps them in VGPRs).  Step j: lane c holds
+// G'[j][c] = G'[c][j], so the scaled pivot row R[j][c] = G'[j][c] / r sits in lane c; it is
+// broadcast through one LDS row SB, all of whose reads issue together (one round trip per
+// step).  A wave issues its LDS operations in order; wave_lds_order keeps the compiler from
+// moving them, so no barrier sits on the chain.  The pivot's square root and reciprocal are
+// the hardware's (1 ulp).
+__device__ __forceinline__ int chol_diag_wave(float* D, float* RT, float* RI, float* SB, int lane) {
+  asm volatile("" : "+v"(lane));  // lane-derived values stay here, not hoisted out of the caller's loop
+  f32x16 v0, v1, v2, v3;
+  auto V = [&](auto qc) -> f32x16& {
+    constexpr int q = decltype(qc)::value;
+    if constexpr (q == 0) return v0;
+    else if constexpr (q == 1) return v1;
+    else if constexpr (q == 2) return v2;
+    else return v3;
+  };
+  static_for<0, 4>([&](auto qc) {
+    constexpr int q = decltype(qc)::value;
+    f32x16& v = V(qc);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int c = 16 * q + e;
+      v[e] = D[(c >= lane) ? lane * 65 + c : c * 65 + lane];
+    }
+  });
+  int fail = INT_MAX;
+  static_for<0, 64>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    constexpr int C0 = (j + 1) / 4;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const float rjj = V(std::integral_constant<int, j / 16>{})[j % 16];
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rjj), j));
+    if (!(d > 0.f) && fail == INT_MAX) fail = j;
+    const float r = __builtin_amdgcn_sqrtf(d), rinv = __builtin_amdgcn_rcpf(r);
+    const float si = (ln == j) ? r : rjj * rinv;  // lane c > j: R[j][c]
+    const float sm = (ln > j) ? si : 0.f;          // rows below j take the update
+    SB[ln] = si;
+    wave_lds_order();
+    if constexpr (C0 < 16) {
+      float4 p[16 - C0];
+#pragma unroll
+      for (int c4 = C0; c4 < 16; ++c4) p[c4 - C0] = reinterpret_cast<const float4*>(SB)[c4];
+#pragma unroll
+      for (int c4 = C0; c4 < 16; ++c4) {
+        const float pv[4] = {p[c4 - C0].x, p[c4 - C0].y, p[c4 - C0].z, p[c4 - C0].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = 4 * c4 + e;
+          if (c > j) {
+            if (c < 16) v0[c] -= sm * pv[e];
+            else if (c < 32) v1[c - 16] -= sm * pv[e];
+            else if (c < 48) v2[c - 32] -= sm * pv[e];
+            else v3[c - 48] -= sm * pv[e];
+          }
+        }
+      }
+    }
+    const float rj = (ln >= j) ? si : 0.f;
+    D[j * 65 + ln] = rj;   // row j of R
+    RT[ln * 68 + j] = rj;  // column ln of R
+    RI[j] = rinv;          // same value from every lane
+    wave_lds_order();      // the next step's SB store stays behind this step's reads
+  });
+  return fail;
+}
+
+// Wave 0: XT = (R^-1)^T (XT[i][k] = Dinv[k][i], row stride 65) for the upper R given column-
+// major in RT (row stride 68), with 1 / R[c][c] in RI.  Lane i forms row i of X = R^-1 from
+// X R = I column by column, X[i][c] = (delta_ic - sum_{k<c} X[i][k] R[k][c]) / R[c][c]; the
+// column of R is a float4 LDS broadcast.  Rows below the diagonal come out as exact zeros.
+// XT may alias RT: it is written only after the last read of RT.
+__device__ __forceinline__ void chol_inverse_wave(const float* RT, const float* RI, float* XT, int lane) {
+  asm volatile("" : "+v"(lane));  // lane-derived values stay here, not hoisted out of the caller's loop
+  float x[64];
+  static_for<0, 64>([&](auto cc) {
+    constexpr int c = decltype(cc)::value;
+    float acc = (lane == c) ? 1.f : 0.f;
+#pragma unroll
+    for (int k4 = 0; k4 < (c + 3) / 4; ++k4) {
+      const float4 rv = reinterpret_cast<const float4*>(RT + c * 68)[k4];
+      const float rvv[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (4 * k4 + e < c) acc -= x[4 * k4 + e] * rvv[e];
+    }
+    x[c] = acc * RI[c];
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  wave_lds_order();
+#pragma unroll
+  for (int c = 0; c < 64; ++c) XT[c * 65 + lane] = x[c];
 }
 
 __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
-  constexpr int NW = kCholThreads / 64, CPW = 64 / NW;
+  constexpr int NW = kCholThreads / 64;
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float* D = smem;                 // [64][65] diagonal block, then R_kk (upper, zero below)
-  float* XT = D + 64 * 65;         // [64][65] (R_kk^-1)^T: XT[i][k] = Dinv_kk[k][i]
-  float* SB = XT + 64 * 65;        // [64] scaled pivot row broadcast (wave 0)
+  float* XT = D + 64 * 65;         // [64][65] (R_kk^-1)^T: XT[i][k] = Dinv_kk[k][i] ...
+  float* RT = XT;                  // ... over [64][68] R_kk column-major while it is factored
+  float* RI = XT + 64 * 68;        // [64] 1 / R[j][j] of the diagonal block
+  float* SB = RI + 64;             // [64] scaled pivot row broadcast (wave 0)
   float* red = SB + 64;            // [16]
   int* ffail = reinterpret_cast<int*>(red + 16);
   float* S = red + 32;             // block row [64][n-64] when strip_lds
@@ -68,114 +171,23 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
   for (int i = tid; i < n; i += kCholThreads) G[(int64_t)i * n + i] += mu;
   __syncthreads();
 
-  for (int k0 = 0; k0 < n; k0 += kCholNb) {
-    const int kb = min(kCholNb, n - k0), k1 = k0 + kb, w = n - k1;
+  // Iteration k0 = -64 has no block of its own: its "trailing update" is wave 0 taking the
+  // first diagonal block from G (so the factor and the inverse exist once in the code).
+  for (int k0 = -kCholNb; k0 < n; k0 += kCholNb) {
+    const bool first = k0 < 0;
+    const int kb = first ? 0 : min(kCholNb, n - k0), k1 = first ? 0 : k0 + kb, w = n - k1;
 
-    // diagonal block (upper part as stored); outside kb an identity pads it
-    for (int idx = tid; idx < 64 * 64; idx += kCholThreads) {
-      const int i = idx >> 6, c = idx & 63;
-      float v = (i == c) ? 1.f : 0.f;
-      if (i < kb && c < kb && c >= i) v = G[(int64_t)(k0 + i) * n + k0 + c];
-      D[i * 65 + c] = v;
-    }
-    __syncthreads();
+    if (!first) {
+      // R_kk (upper) and Dinv_kk (row-major, zero below the diagonal) to HBM
+      for (int idx = tid; idx < kb * 64; idx += kCholThreads) {
+        const int i = idx >> 6, c = idx & 63;
+        if (c < kb && c >= i) G[(int64_t)(k0 + i) * n + k0 + c] = D[i * 65 + c];
+        Dv[(int64_t)(k0 + i) * 64 + c] = (c < kb) ? XT[c * 65 + i] : 0.f;
+      }
+      if (w <= 0) break;  // uniform; kb == 64 below this line
 
-    if (wid == 0) {
-      // lane i holds symmetric row i of the block; step j broadcasts the scaled pivot row
-      // R[j][c] = G'[j][c] / r (held by lane c) through LDS inside the wave.  A wave issues
-      // its LDS operations in order and the store/load addresses may alias, so neither the
-      // hardware nor the compiler reorders them: no fence or barrier sits on the chain.
-      // the row is four named 16-wide vectors (element access with compile-time indices), so
-      // it stays in VGPRs whatever the unrolled code around it looks like
-      f32x16 v0, v1, v2, v3;
-      auto V = [&](auto qc) -> f32x16& {
-        constexpr int q = decltype(qc)::value;
-        if constexpr (q == 0) return v0;
-        else if constexpr (q == 1) return v1;
-        else if constexpr (q == 2) return v2;
-        else return v3;
-      };
-      static_for<0, 4>([&](auto qc) {
-        constexpr int q = decltype(qc)::value;
-        f32x16& v = V(qc);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int c = 16 * q + e;
-          v[e] = D[(c >= lane) ? lane * 65 + c : c * 65 + lane];
-        }
-      });
-      int fail = INT_MAX;
-      static_for<0, 64>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        const float rjj = V(std::integral_constant<int, j / 16>{})[j % 16];
-        const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rjj), j));
-        if (!(d > 0.f) && fail == INT_MAX) fail = j;
-        const float r = sqrtf(d), rinv = 1.f / r;
-        const float si = (ln == j) ? r : rjj * rinv;  // lane c > j: R[j][c]
-        const float sm = (ln > j) ? si : 0.f;          // rows below j take the update
-        SB[ln] = si;
-        // 16 broadcast values at a time (scheduling barriers keep the reads from all being
-        // hoisted at once)
-        static_for<(j + 1) / 16, 4>([&](auto qc) {
-          constexpr int q = decltype(qc)::value;
-          f32x16& v = V(qc);
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            if (16 * q + e > j) v[e] -= sm * SB[16 * q + e];
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        });
-        D[j * 65 + ln] = (ln >= j) ? si : 0.f;  // row j of R
-        __builtin_amdgcn_sched_barrier(0);
-      });
-      if (lane == 0 && fail != INT_MAX && fail < kb && *ffail == INT_MAX) *ffail = k0 + fail + 1;
-    }
-    __syncthreads();
-
-    // Dinv_kk = R_kk^-1 by back substitution: wave w solves columns w*CPW.., lane i holding
-    // row i of R and entry i of the running right-hand side
-    {
-      float rr[64];
-#pragma unroll
-      for (int c = 0; c < 64; ++c) rr[c] = D[lane * 65 + c];  // R_kk is zero below the diagonal
-      const float rd = 1.f / D[lane * 65 + lane];  // 1 / R[i][i] in lane i
-      float x[CPW];
-      const int cw = __builtin_amdgcn_readfirstlane(wid * CPW);
-#pragma unroll
-      for (int u = 0; u < CPW; ++u) x[u] = (lane == cw + u) ? 1.f : 0.f;
-      static_for<0, 64>([&](auto kc) {
-        constexpr int k = 63 - decltype(kc)::value;  // k = 63 .. 0
-        int ln = lane, c0w = cw;
-        asm volatile("" : "+v"(ln), "+s"(c0w));
-        const float rk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rd), k));
-        const float mr = (ln < k) ? rr[k] : 0.f;  // rows above k take the update
-#pragma unroll
-        for (int u = 0; u < CPW; ++u) {
-          if (k <= c0w + u) {
-            const float xk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[u]), k)) * rk;
-            x[u] = (ln == k) ? xk : x[u] - mr * xk;
-          }
-        }
-      });
-      // column cw+u of the inverse -> XT[cw+u][i]
-#pragma unroll
-      for (int u = 0; u < CPW; ++u) XT[(cw + u) * 65 + lane] = (lane <= cw + u) ? x[u] : 0.f;
-    }
-    __syncthreads();
-
-    // R_kk (upper) and Dinv_kk (row-major, zero below the diagonal) to HBM
-    for (int idx = tid; idx < kb * 64; idx += kCholThreads) {
-      const int i = idx >> 6, c = idx & 63;
-      if (c < kb && c >= i) G[(int64_t)(k0 + i) * n + k0 + c] = D[i * 65 + c];
-      Dv[(int64_t)(k0 + i) * 64 + c] = (c < kb) ? XT[c * 65 + i] : 0.f;
-    }
-    if (w <= 0) break;  // uniform; kb == 64 below this line
-
-    // block row R_k,> = Dinv_kk^T G_k,>: each wave owns 32 columns (both 32-row halves),
-    // so it can overwrite them in G without racing other waves' reads.
-    {
+      // block row R_k,> = Dinv_kk^T G_k,>: each wave owns 32 columns (both 32-row halves),
+      // so it can overwrite them in G without racing other waves' reads.
       const int nch = (w + 31) >> 5;
       for (int job = wid; job < nch; job += NW) {
         const int colr = job * 32 + l32, col = k1 + colr;
@@ -203,13 +215,16 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
           }
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
 
-    // trailing G_>,> -= R_k,>^T R_k,> over upper 64x64 tiles, one tile per wave at a time
+    // trailing G_>,> -= R_k,>^T R_k,> over upper 64x64 tiles.  Tile 0 is the next diagonal
+    // block: wave 0 keeps it in LDS and factors and inverts it; waves 1..7 take the other
+    // tiles and write them back to G.
     {
-      const int nt = (w + 63) >> 6, npairs = nt * (nt + 1) / 2;
-      for (int pr = wid; pr < npairs; pr += NW) {
+      const int nt = (w + 63) >> 6, npairs = first ? 1 : nt * (nt + 1) / 2;
+      const int t0 = wid == 0 ? 0 : wid, tstep = wid == 0 ? npairs : NW - 1;
+      for (int pr = t0; pr < npairs; pr += tstep) {
         int I, J;
         upper_tile(pr, nt, I, J);
         f32x16 acc[2][2];
@@ -223,36 +238,57 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
               const int col = k1 + J * 64 + nj * 32 + l32;
               acc[mi][nj][r] = (row < n && col < n) ? G[(int64_t)row * n + col] : 0.f;
             }
+        if (!first) {
 #pragma unroll 4
-        for (int kk = 0; kk < kCholNb; kk += 2) {
-          const int k = kk + h;
-          float av[2], bv[2];
+          for (int kk = 0; kk < kCholNb; kk += 2) {
+            const int k = kk + h;
+            float av[2], bv[2];
 #pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            const int ci = I * 64 + q * 32 + l32, cj = J * 64 + q * 32 + l32;
-            if (a.strip_lds) {
-              av[q] = (ci < w) ? -S[k * lds_w + ci] : 0.f;
-              bv[q] = (cj < w) ? S[k * lds_w + cj] : 0.f;
-            } else {
-              av[q] = (ci < w) ? -G[(int64_t)(k0 + k) * n + k1 + ci] : 0.f;
-              bv[q] = (cj < w) ? G[(int64_t)(k0 + k) * n + k1 + cj] : 0.f;
+            for (int q = 0; q < 2; ++q) {
+              const int ci = I * 64 + q * 32 + l32, cj = J * 64 + q * 32 + l32;
+              if (a.strip_lds) {
+                av[q] = (ci < w) ? -S[k * lds_w + ci] : 0.f;
+                bv[q] = (cj < w) ? S[k * lds_w + cj] : 0.f;
+              } else {
+                av[q] = (ci < w) ? -G[(int64_t)(k0 + k) * n + k1 + ci] : 0.f;
+                bv[q] = (cj < w) ? G[(int64_t)(k0 + k) * n + k1 + cj] : 0.f;
+              }
             }
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+              for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = mfma(av[mi], bv[nj], acc[mi][nj]);
           }
+        }
+        if (pr == 0) {
+          // next diagonal block -> D (identity past n), then factor and invert it
+          const int kbn = min(kCholNb, w);
 #pragma unroll
           for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-            for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = mfma(av[mi], bv[nj], acc[mi][nj]);
+            for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int i = mi * 32 + acc_row(r, lane), c = nj * 32 + l32;
+                D[i * 65 + c] = (i < kbn && c < kbn) ? acc[mi][nj][r] : (i == c ? 1.f : 0.f);
+              }
+          wave_lds_order();
+          const int fail = chol_diag_wave(D, RT, RI, SB, lane);
+          if (lane == 0 && fail != INT_MAX && fail < kbn && *ffail == INT_MAX) *ffail = k1 + fail + 1;
+          wave_lds_order();
+          chol_inverse_wave(RT, RI, XT, lane);
+        } else {
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int row = k1 + I * 64 + mi * 32 + acc_row(r, lane);
+                const int col = k1 + J * 64 + nj * 32 + l32;
+                if (row < n && col < n) G[(int64_t)row * n + col] = acc[mi][nj][r];
+              }
         }
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-          for (int nj = 0; nj < 2; ++nj)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int row = k1 + I * 64 + mi * 32 + acc_row(r, lane);
-              const int col = k1 + J * 64 + nj * 32 + l32;
-              if (row < n && col < n) G[(int64_t)row * n + col] = acc[mi][nj][r];
-            }
       }
     }
     __syncthreads();

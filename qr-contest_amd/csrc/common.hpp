@@ -105,6 +105,45 @@ __device__ __forceinline__ void wave_argmax(float& babs, float& bv, int& bi) {
   bi = ri;
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Wave-wide maximum of an unsigned 64-bit key (all 64 lanes active); the result is uniform.
+// Four DPP butterflies reduce each row of 16 lanes, the four rows are combined by readlane.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  uint64_t o;
+  o = dpp_u64<kDppQuad1032>(v); v = o > v ? o : v;
+  o = dpp_u64<kDppQuad2301>(v); v = o > v ? o : v;
+  o = dpp_u64<kDppRowHalfMirror>(v); v = o > v ? o : v;
+  o = dpp_u64<kDppRowMirror>(v); v = o > v ? o : v;
+  uint64_t r = readlane_u64(v, 0);
+#pragma unroll
+  for (int row = 1; row < 4; ++row) {
+    const uint64_t t = readlane_u64(v, 16 * row);
+    r = t > r ? t : r;
+  }
+  return r;
+}
+
+// Component I of a float4 (compile-time I).
+template <int I>
+__device__ __forceinline__ float f4get(const float4& v) {
+  if constexpr (I == 0) return v.x;
+  else if constexpr (I == 1) return v.y;
+  else if constexpr (I == 2) return v.z;
+  else return v.w;
+}
+
 // Calls f(std::integral_constant<int, I>) for I = B .. E-1, fully unrolled at compile time
 // (register arrays indexed by I then stay in registers).
 template <int B, int E, typename F>

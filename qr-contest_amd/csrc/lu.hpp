@@ -53,8 +53,12 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
 
 inline int lu_panel_nb(int n) { return n <= 512 ? 64 : (n <= 1024 ? 32 : 16); }
 
+// panel [n][nb+1] | -U12 chunk [nb][64] | row map [n] | pivot keys [3] (u64) | per-wave
+// candidate slots [2][8][nb+4]
 inline size_t lu_lds_bytes(int n, int nb) {
-  return sizeof(float) * ((size_t)n * (nb + 1) + (size_t)nb * 64 + (size_t)n + 4);
+  const size_t p = ((size_t)n * (nb + 1) + 3) & ~(size_t)3;
+  const size_t pl = ((size_t)n + 3) & ~(size_t)3;
+  return sizeof(float) * (p + (size_t)nb * 64 + pl + 8 + 2 * 8 * (size_t)(nb + 4));
 }
 
 template <bool PIVOT, int NB, int RPT>
@@ -67,11 +71,11 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   const int n = a.n;
   float* P = smem;                                  // panel [n][NB+1]
-  float* U = P + (((size_t)n * LDP + 3) & ~(size_t)3);  // -U12 chunk [NB][64]; panel-phase scratch
+  float* U = P + (((size_t)n * LDP + 3) & ~(size_t)3);  // -U12 chunk [NB][64]
   int* pl = reinterpret_cast<int*>(U + NB * 64);    // logical -> physical row
-  float4* PB4 = reinterpret_cast<float4*>(U);       // [2][NB/4] pivot row
-  float4* PJ4 = PB4 + 2 * NB4;                      // [2][NB/4] displaced row j
-  float2* red = reinterpret_cast<float2*>(U + 4 * NB);  // [2][NW] (value, index bits)
+  unsigned long long* pkeys =                       // [3] pivot keys (LU), by step mod 3
+      reinterpret_cast<unsigned long long*>(reinterpret_cast<float*>(pl) + ((n + 3) & ~3));
+  float* slots = reinterpret_cast<float*>(pkeys) + 8;  // [2][NW][NB+4] candidate rows
 
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5, l16 = lane & 15, q4 = lane >> 4;
@@ -81,6 +85,8 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
 
   if (PIVOT)
     for (int i = tid; i < n; i += T) pl[i] = i;
+  if (tid < 3) pkeys[tid] = 0ull;
+  int step = 0;  // LU column steps so far (selects the pivot key buffer)
   __syncthreads();
 
   for (int k0 = 0; k0 < n; k0 += NB) {
@@ -128,145 +134,139 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
       for (int c = 0; c < NB; ++c) row[q][c] = (r < m) ? P[sw(r, c)] : 0.f;
     }
 
-    // ---- factor the panel column by column (compile-time column index).  Columns past kb
-    //      (last panel only) are no-ops: rows >= m are zero and none is below row j >= m.
+    // ---- factor the panel column by column (compile-time column index).  One barrier per
+    //      column.  Rows stay in their threads: pos[q] is the logical position (relative to
+    //      k0) of the row a thread holds, and a pivot choice only swaps two labels.  Each
+    //      wave publishes its best candidate key in one LDS atomic maximum and the candidate
+    //      row in a per-wave slot (double-buffered by column parity), so after the barrier
+    //      every thread finds the pivot and reads its row.  Waves whose rows all lie at or
+    //      past m (finished rows) only take part in the barriers.
+    const int nwa = min(NW, (m + 63) >> 6);  // waves holding rows < m
+    const bool wact = wid < nwa;
+    int pos[RPT], phys[RPT];
+#pragma unroll
+    for (int q = 0; q < RPT; ++q) {
+      const int r = tid + T * q;
+      pos[q] = r;
+      phys[q] = (PIVOT && r < m) ? pl[k0 + r] : 0;
+    }
+    constexpr int SLOT4 = NB4 + 1;  // float4 units per slot: one spare + the row
+    float4* slot4 = reinterpret_cast<float4*>(slots);
     int buf = 0;
     float my_s = 1.f;
     static_for<0, NB>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
-      {
+      constexpr int C0 = j / 4;  // first chunk holding a column >= j
+      if (j < kb) {  // uniform
         // the row index is laundered through an empty asm each column so that the per-column
-        // lane masks (r > j, r >= j) are formed here instead of being hoisted for all NB
-        // columns to the kernel start (which spills ~1000 SGPRs)
+        // lane masks are formed here instead of being hoisted for all NB columns to the
+        // kernel start (which spills ~1000 SGPRs)
         int rbase = tid;
         asm volatile("" : "+v"(rbase));
+        float4* sb = slot4 + buf * NW * SLOT4;
+        float4 pr4[NB4 - C0];
         float l[RPT];
         if constexpr (PIVOT) {
-          float bv = 0.f, babs = -1.f;
-          int bi = INT_MAX;
+          // key: candidates (rows at positions >= j) rank by |v| (NaN lowest), ties by the
+          // smaller position (LAPACK's first maximum); the low 4 bits name the wave.  Key
+          // buffer = step mod 3; the next step's buffer is cleared now (its last readers
+          // finished two barriers ago).
+          unsigned long long* kcur = pkeys + step % 3;
+          if (tid == 0) pkeys[(step + 1) % 3] = 0ull;
+          ++step;
+          if (wact) {
+            uint64_t best = 0;
+            int bq = 0;
 #pragma unroll
-          for (int q = 0; q < RPT; ++q) {
-            const int r = rbase + T * q;
-            const float v = row[q][j], av = fabsf(v);
-            if (r >= j && r < m && av > babs) { babs = av; bv = v; bi = r; }
-          }
-          wave_argmax(babs, bv, bi);
-          if (lane == 0) red[buf * NW + wid] = make_float2(bv, __int_as_float(bi));
-          __syncthreads();
-          // the NW wave winners in one batch of LDS reads, then a branch-free reduction
-          // (a wave without candidates reports index INT_MAX and ranks below any row)
-          float4 e4[NW / 2];
-#pragma unroll
-          for (int w = 0; w < NW / 2; ++w) e4[w] = reinterpret_cast<const float4*>(red + buf * NW)[w];
-          float pv = e4[0].x, pabs;
-          int p = __float_as_int(e4[0].y);
-          pabs = (p == INT_MAX) ? -1.f : fabsf(pv);
-#pragma unroll
-          for (int w = 1; w < NW; ++w) {
-            const float v = (w & 1) ? e4[w / 2].z : e4[w / 2].x;
-            const int i = __float_as_int((w & 1) ? e4[w / 2].w : e4[w / 2].y);
-            argmax_take(pabs, pv, p, (i == INT_MAX) ? -1.f : fabsf(v), v, i);
-          }
-          p = __builtin_amdgcn_readfirstlane(p);
-          pv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(pv)));
-          if (p == INT_MAX) { p = j; pv = __int_as_float(0x7fc00000); }  // all-NaN column
-          const int po = p % T, pq = p / T;
-          if (tid == po) {
-#pragma unroll
-            for (int q = 0; q < RPT; ++q)
-              if (q == pq) {
-#pragma unroll
-                for (int c4 = 0; c4 < NB4; ++c4)
-                  PB4[buf * NB4 + c4] = make_float4(row[q][4 * c4], row[q][4 * c4 + 1],
-                                                    row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
-              }
-          }
-          if (p != j && tid == j) {
-#pragma unroll
-            for (int c4 = 0; c4 < NB4; ++c4)
-              PJ4[buf * NB4 + c4] = make_float4(row[0][4 * c4], row[0][4 * c4 + 1],
-                                                row[0][4 * c4 + 2], row[0][4 * c4 + 3]);
-          }
-          __syncthreads();
-          if (p != j) {
-            if (tid == j) {
-#pragma unroll
-              for (int c4 = 0; c4 < NB4; ++c4) {
-                const float4 t = PB4[buf * NB4 + c4];
-                row[0][4 * c4] = t.x; row[0][4 * c4 + 1] = t.y;
-                row[0][4 * c4 + 2] = t.z; row[0][4 * c4 + 3] = t.w;
-              }
+            for (int q = 0; q < RPT; ++q) {
+              const int r = rbase + T * q;
+              const float v = row[q][j];
+              const bool cand = r < m && pos[q] >= j;
+              const uint32_t kb32 = cand ? (v != v ? 1u : __float_as_uint(fabsf(v)) + 2u) : 0u;
+              const uint64_t key = ((uint64_t)kb32 << 32) | (uint32_t)(((2047 - pos[q]) << 4) | wid);
+              if (key > best) { best = key; bq = q; }
             }
-            if (tid == po) {
+            const uint64_t wbest = wave_max_u64(best);
+            if (best == wbest) {  // exactly one lane: keys are distinct
+              atomicMax(kcur, (unsigned long long)wbest);
 #pragma unroll
               for (int q = 0; q < RPT; ++q)
-                if (q == pq) {
+                if (q == bq) {
 #pragma unroll
-                  for (int c4 = 0; c4 < NB4; ++c4) {
-                    const float4 t = PJ4[buf * NB4 + c4];
-                    row[q][4 * c4] = t.x; row[q][4 * c4 + 1] = t.y;
-                    row[q][4 * c4 + 2] = t.z; row[q][4 * c4 + 3] = t.w;
-                  }
+                  for (int c4 = C0; c4 < NB4; ++c4)
+                    sb[wid * SLOT4 + 1 + c4] = make_float4(row[q][4 * c4], row[q][4 * c4 + 1],
+                                                           row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
                 }
             }
-            if (tid == 0) {
-              const int t = pl[k0 + j];
-              pl[k0 + j] = pl[k0 + p];
-              pl[k0 + p] = t;
+          }
+          __syncthreads();
+          if (wact) {
+            const uint64_t pk = *kcur;
+            const int pw = (int)(pk & 15u);
+            const int p = 2047 - (int)((uint32_t)pk >> 4);
+#pragma unroll
+            for (int c4 = C0; c4 < NB4; ++c4) pr4[c4 - C0] = sb[pw * SLOT4 + 1 + c4];
+            const float pv = f4get<j % 4>(pr4[0]);
+            // LAPACK xGETRF2: scale by the reciprocal unless the pivot is subnormal; a zero
+            // pivot leaves the column as it is (then every candidate is zero: no update)
+            const bool nz = pv != 0.f;
+            const bool recip = fabsf(pv) >= 1.17549435e-38f;
+            const float inv = 1.f / pv;
+#pragma unroll
+            for (int q = 0; q < RPT; ++q) {
+              const int r = rbase + T * q;
+              const bool below = r < m && pos[q] >= j && pos[q] != p;
+              l[q] = 0.f;
+              if (below) {
+                l[q] = row[q][j];
+                if (nz) {
+                  l[q] = recip ? l[q] * inv : l[q] / pv;
+                  row[q][j] = l[q];
+                }
+              }
+              pos[q] = (pos[q] == p) ? j : ((pos[q] == j) ? p : pos[q]);
             }
           }
-          // LAPACK xGETRF2: scale by the reciprocal unless the pivot is subnormal; a zero
-          // pivot leaves the column as it is (its update is then a no-op).
-          const bool nz = pv != 0.f;
-          const bool recip = fabsf(pv) >= 1.17549435e-38f;
-          const float inv = 1.f / pv;
+        } else {
+          // chart: the pivot row is row j (held by thread j, j < NB <= T)
+          if (tid == j) {
 #pragma unroll
-          for (int q = 0; q < RPT; ++q) {
-            const int r = rbase + T * q;
-            l[q] = 0.f;
-            if (r > j && r < m) {
-              l[q] = row[q][j];
-              if (nz) {
-                l[q] = recip ? l[q] * inv : l[q] / pv;
+            for (int c4 = C0; c4 < NB4; ++c4)
+              sb[1 + c4] = make_float4(row[0][4 * c4], row[0][4 * c4 + 1], row[0][4 * c4 + 2],
+                                       row[0][4 * c4 + 3]);
+          }
+          __syncthreads();
+          if (wact) {
+#pragma unroll
+            for (int c4 = C0; c4 < NB4; ++c4) pr4[c4 - C0] = sb[1 + c4];
+            const float d = f4get<j % 4>(pr4[0]);
+            const float pp = 1.f - d, pm = 1.f + d;
+            const bool plus = fabsf(pp) >= fabsf(pm);  // |1-d| >= |1+d|: the tie d = 0 takes +1
+            const float sk = plus ? 1.f : -1.f;
+            const float piv = plus ? pp : pm;
+            if (tid == j) my_s = sk;
+#pragma unroll
+            for (int q = 0; q < RPT; ++q) {
+              const int r = rbase + T * q;
+              l[q] = 0.f;
+              if (r > j && r < m) {
+                l[q] = (-sk * row[q][j]) / piv;
                 row[q][j] = l[q];
               }
             }
           }
-        } else {
-          if (tid == j) {
-#pragma unroll
-            for (int c4 = 0; c4 < NB4; ++c4)
-              PB4[buf * NB4 + c4] = make_float4(row[0][4 * c4], row[0][4 * c4 + 1],
-                                                row[0][4 * c4 + 2], row[0][4 * c4 + 3]);
-          }
-          __syncthreads();
-          const float d = U[buf * NB + j];
-          const float pp = 1.f - d, pm = 1.f + d;
-          const bool plus = fabsf(pp) >= fabsf(pm);
-          const float sk = plus ? 1.f : -1.f;
-          const float piv = plus ? pp : pm;
-          if (tid == j) my_s = sk;
-#pragma unroll
-          for (int q = 0; q < RPT; ++q) {
-            const int r = rbase + T * q;
-            l[q] = 0.f;
-            if (r > j && r < m) {
-              l[q] = (-sk * row[q][j]) / piv;
-              row[q][j] = l[q];
-            }
-          }
         }
-        // rank-1 update of the columns right of j (rows outside (j, m) have l = 0)
+        if (wact) {
+          // rank-1 update of the columns right of j
 #pragma unroll
-        for (int c4 = (j + 1) / 4; c4 < NB4; ++c4) {
-          const float4 pc = PB4[buf * NB4 + c4];
-          const float pcv[4] = {pc.x, pc.y, pc.z, pc.w};
+          for (int c4 = C0; c4 < NB4; ++c4) {
+            const float pcv[4] = {pr4[c4 - C0].x, pr4[c4 - C0].y, pr4[c4 - C0].z, pr4[c4 - C0].w};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int c = 4 * c4 + e;
-            if (c > j) {
+            for (int e2 = 0; e2 < 4; ++e2) {
+              if (4 * c4 + e2 > j) {
 #pragma unroll
-              for (int q = 0; q < RPT; ++q) row[q][c] -= l[q] * pcv[e];
+                for (int q = 0; q < RPT; ++q) row[q][4 * c4 + e2] -= l[q] * pcv[e2];
+              }
             }
           }
         }
@@ -274,13 +274,14 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
       }
     });
 
-    // ---- registers -> LDS panel
+    // ---- registers -> LDS panel, each row at its logical position; the row map follows
 #pragma unroll
     for (int q = 0; q < RPT; ++q) {
       const int r = tid + T * q;
       if (r < m) {
 #pragma unroll
-        for (int c = 0; c < NB; ++c) P[sw(r, c)] = row[q][c];
+        for (int c = 0; c < NB; ++c) P[sw(pos[q], c)] = row[q][c];
+        if (PIVOT) pl[k0 + pos[q]] = phys[q];
       }
     }
     if (!PIVOT && tid < kb) a.s[(int64_t)b * n + k0 + tid] = my_s;
