@@ -14,8 +14,8 @@
 //     inside the wave, no barriers) and forms its inverse (lane i computes row i of R^-1 by
 //     forward substitution over LDS broadcasts of R's columns), while waves 1..7 update the
 //     other tiles.  The sequential diagonal work thus runs under the trailing update.
-// The diagonal-block inverses go to Dinv ([n][64] per matrix) for the triangular solve
-// that follows.  info records the first column whose pivot was not positive (1-based; NaN
+// The diagonal-block inverses go to Dinv ([n][64] per matrix) for the triangular solve that
+// follows.  info records the first column whose pivot was not positive (1-based; NaN
 // counts as not positive).
 #pragma once
 #include "common.hpp"

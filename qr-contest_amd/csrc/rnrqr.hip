@@ -4,9 +4,11 @@
 //   1. k_lu<true>        A -> W (in-place factor, A's row order), perm, L      (:66)
 //   2. k_tn_upper        G = L^T L, upper tiles, zero rows of L skipped         (:73)
 //   3. k_chol            G -> R_a (upper, jittered), Dinv, info                 (:74-76)
-//   4. k_trsm            Q1 = L R_a^-1 -> W                                     (:77)
+//      k_wblocks         W = off-diagonal blocks of R_a times Dinv -> Qb (the solve's operand)
+//   4. k_trsm            Q1 = L R_a^-1 -> L buffer                              (:77)
 //   5. k_tn_upper        G = Q1^T Q1                                            (:73)
 //   6. k_chol            G -> R_b, Dinv, info                                   (:74-76)
+//      k_wblocks         W for R_b -> the (now dead) LU buffer
 //   7. k_trsm            Q = P (Q1 R_b^-1) -> Qb and H (row scatter)            (:77,81)
 //   8. k_lu<false>       chart in place on H: tails Y, signs s, tau             (:139-174,192)
 //   9. k_tn_upper        H_upper = diag(s) triu(Q^T A), masked to j >= i         (:186,195)
@@ -75,8 +77,8 @@ size_t carve(int64_t batch, int64_t n, unsigned need, char* base, Ws* ws) {
 
 constexpr unsigned kQrNeed = kNeedW | kNeedL | kNeedG | kNeedQb | kNeedDinv | kNeedS | kNeedPerm | kNeedInfo;
 constexpr unsigned kLuNeed = kNeedW;
-constexpr unsigned kCholqrNeed = kNeedG | kNeedDinv | kNeedInfo;
-constexpr unsigned kFrameNeed = kNeedW | kNeedL | kNeedG | kNeedDinv | kNeedPerm | kNeedInfo;
+constexpr unsigned kCholqrNeed = kNeedG | kNeedQb | kNeedDinv | kNeedInfo;
+constexpr unsigned kFrameNeed = kNeedW | kNeedL | kNeedG | kNeedQb | kNeedDinv | kNeedPerm | kNeedInfo;
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
@@ -153,27 +155,46 @@ int launch_tn(bool closure, const float* X, int64_t sx, const float* Y, int64_t 
   return hip_status();
 }
 
-int launch_chol(float* G, int64_t sg, float* Dinv, int* info, int64_t batch, int n, bool keep_info,
-                hipStream_t st) {
+// W[k][c] = R[k][c] Dinv_c for the 64-block pairs k < c (the solve's off-diagonal operand)
+int launch_wblocks(const float* R, int64_t sr, const float* Dinv, float* Wm, int64_t batch, int n,
+                   hipStream_t st) {
+  const int nblk = (n + 63) / 64;
+  if (nblk < 2) return RNR_OK;
+  WblkArgs a;
+  a.R = R; a.sr = sr; a.Dinv = Dinv; a.Wm = Wm; a.sw = (int64_t)n * n; a.n = n;
+  a.ncol = nblk - 1;
+  a.vec4 = (n % 4 == 0) && (sr % 4 == 0) && aligned(R, 16);
+  const int64_t total = batch * a.ncol;
+  if (total > INT32_MAX) return RNR_ERR_INVALID_ARG;
+  a.total = (int)total;
+  k_wblocks<<<dim3((unsigned)total), dim3(256), 0, st>>>(a);
+  return hip_status();
+}
+
+int launch_chol(float* G, int64_t sg, float* Dinv, float* Wm, int* info, int64_t batch, int n,
+                bool keep_info, hipStream_t st) {
   CholArgs a;
-  a.G = G; a.sg = sg; a.Dinv = Dinv; a.info = info; a.n = n; a.keep_info = keep_info ? 1 : 0;
+  a.G = G; a.sg = sg; a.Dinv = Dinv; a.info = info; a.n = n;
+  a.keep_info = keep_info ? 1 : 0;
   a.strip_lds = chol_lds_bytes(n, true) <= kLdsMax ? 1 : 0;
   const size_t lds = chol_lds_bytes(n, a.strip_lds != 0);
   if (int e = set_lds(k_chol, lds)) return e;
   k_chol<<<dim3((unsigned)batch), dim3(kCholThreads), lds, st>>>(a);
-  return hip_status();
+  if (int e = hip_status()) return e;
+  return launch_wblocks(G, sg, Dinv, Wm, batch, n, st);
 }
 
-int launch_trsm(const float* M, int64_t sm, const int* mperm, const float* R, int64_t sr,
+int launch_trsm(const float* M, int64_t sm, const int* mperm, const float* Wm, int64_t sw,
                 const float* Dinv, float* Q, int64_t sq, float* Q2, int64_t sq2, const int* perm,
                 int64_t batch, int n, hipStream_t st) {
   TrsmArgs a;
-  a.M = M; a.sm = sm; a.R = R; a.sr = sr; a.Dinv = Dinv; a.Q = Q; a.sq = sq; a.Q2 = Q2; a.sq2 = sq2;
+  a.M = M; a.sm = sm; a.Wm = Wm; a.sw = sw; a.Dinv = Dinv; a.Q = Q; a.sq = sq; a.Q2 = Q2; a.sq2 = sq2;
   a.perm = perm; a.mperm = mperm; a.n = n; a.nrb = (n + kTrsmRows - 1) / kTrsmRows;
   const int64_t total = batch * a.nrb;
   if (total > INT32_MAX) return RNR_ERR_INVALID_ARG;
   a.total = (int)total;
-  const bool vec4 = (n % 4 == 0) && (sq % 4 == 0) && (sr % 4 == 0) && aligned(Q, 16) && aligned(R, 16);
+  const bool vec4 = (n % 4 == 0) && (sq % 4 == 0) && (sm % 4 == 0) && aligned(Q, 16) && aligned(M, 16) &&
+                    aligned(Wm, 16);
   if (vec4)
     k_trsm<true><<<dim3((unsigned)total), dim3(256), 0, st>>>(a);
   else
@@ -211,7 +232,7 @@ bool small_path(int64_t n) { return n <= kSmallMaxN; }
 
 // One CholeskyQR pass: Q = M chol(M^T M + mu I)^-1, R left in G.  With lperm, M is the unit-
 // lower L held in A's row order (the LU's in-place factor) and is read through lperm.
-int cholqr_pass(const float* M, int64_t sm, const int* lperm, float* G, float* Dinv, int* info,
+int cholqr_pass(const float* M, int64_t sm, const int* lperm, float* G, float* Dinv, float* Wm, int* info,
                 bool keep_info, float* Q, float* Q2, const int* perm, int64_t batch, int n,
                 hipStream_t st, Marks& mk) {
   const int64_t nn = (int64_t)n * n;
@@ -219,9 +240,9 @@ int cholqr_pass(const float* M, int64_t sm, const int* lperm, float* G, float* D
   if (int e = launch_tn(false, M, sm, M, sm, G, nn, nullptr, lperm, batch, n, lperm != nullptr, st))
     return e;
   if (int e = mk.mark(st)) return e;
-  if (int e = launch_chol(G, nn, Dinv, info, batch, n, keep_info, st)) return e;
+  if (int e = launch_chol(G, nn, Dinv, Wm, info, batch, n, keep_info, st)) return e;
   if (int e = mk.mark(st)) return e;
-  return launch_trsm(M, sm, lperm, G, nn, Dinv, Q, nn, Q2, nn, perm, batch, n, st);
+  return launch_trsm(M, sm, lperm, Wm, nn, Dinv, Q, nn, Q2, nn, perm, batch, n, st);
 }
 
 // The frame: LU of A in place into ws.W (+ ws.perm), CholeskyQR2 of L read through perm,
@@ -231,10 +252,12 @@ int frame(const float* A, int64_t sa, const Ws& w, float* Q, float* Qcopy, int* 
   const int64_t nn = (int64_t)n * n;
   if (int e = mk.mark(st)) return e;
   if (int e = launch_lu(true, A, sa, w.W, nn, batch, n, w.perm, nullptr, nullptr, nullptr, st)) return e;
-  if (int e = cholqr_pass(w.W, nn, w.perm, w.G, w.Dinv, info, false, w.L, nullptr, nullptr, batch, n,
+  // W (the solve's off-diagonal operand) lives in Qb for the first pass and in the then
+  // dead LU buffer for the second
+  if (int e = cholqr_pass(w.W, nn, w.perm, w.G, w.Dinv, w.Qb, info, false, w.L, nullptr, nullptr, batch, n,
                           st, mk))
     return e;
-  return cholqr_pass(w.L, nn, nullptr, w.G, w.Dinv, info, true, Q, Qcopy, w.perm, batch, n, st, mk);
+  return cholqr_pass(w.L, nn, nullptr, w.G, w.Dinv, w.W, info, true, Q, Qcopy, w.perm, batch, n, st, mk);
 }
 
 // The whole path (see the launch list at the top of this file).
@@ -353,7 +376,7 @@ int rnr_cholqr_f32(const float* M, int64_t batch, int64_t n, int64_t batch_strid
   carve(batch, n, kCholqrNeed, static_cast<char*>(ws), &w);
   float* G = R ? R : w.G;
   Marks mk{nullptr, 0, 0};
-  return cholqr_pass(M, batch_stride, nullptr, G, w.Dinv, info ? info : w.info, false, Q, nullptr,
+  return cholqr_pass(M, batch_stride, nullptr, G, w.Dinv, w.Qb, info ? info : w.info, false, Q, nullptr,
                      nullptr, batch, (int)n, reinterpret_cast<hipStream_t>(stream), mk);
 }
 
