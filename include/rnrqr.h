@@ -22,6 +22,7 @@
  *   rnr_lu_f32      torch.linalg.lu(A) (P, L; U dropped) reflection_no_reflectors.py:66
  *   rnr_cholqr_f32  _cholqr(M) -> M R^-1                 reflection_no_reflectors.py:68-77
  *   rnr_chart_f32   _chart(Q) -> (Y, s), tau recompute   reflection_no_reflectors.py:86-176,192
+ *   rnr_check_f64   check / check_percol (fp64 gates)    common/oracle.py:152-195
  */
 #ifndef RNRQR_H
 #define RNRQR_H
@@ -109,6 +110,21 @@ int rnr_frame_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride
  * signs (+1/-1) and tau = 2 / (1 + sum_{i>k} Y[i][k]^2).  No workspace. */
 int rnr_chart_f32(float* Y, int64_t batch, int64_t n, float* s, float* tau,
                   rnr_stream_t stream);
+
+/* ---- consumer of the path's output: the contest gates, evaluated on the GPU -------------
+ * fp64 restatement of the reference checker (common/oracle.py:152-195, check and
+ * check_percol): Q = householder_product(H, tau) in float64, then per matrix
+ *   factor[b]   = ||triu(H) - Q^T A||_1 / ||A||_1                               (gate 20 n eps32)
+ *   ortho[b]    = ||Q^T Q - I||_1                                              (gate 100 n eps32)
+ *   colratio[b] = max_j ||(triu(H) - Q^T A)[:, j]||_1 / (20 n eps32 ||A[:, j]||_1)   (gate 1)
+ * with the matrix 1-norm (largest absolute column sum).  A has batch stride batch_stride;
+ * H (batch x n x n) and tau (batch x n) are contiguous; colratio may be NULL.  The result is
+ * the same on every run (no atomics).  Workspace: rnr_check_f64_workspace bytes, 256-byte
+ * aligned. */
+int rnr_check_f64_workspace(int64_t batch, int64_t n, size_t* bytes);
+int rnr_check_f64(const float* A, int64_t batch_stride, const float* H, const float* tau,
+                  int64_t batch, int64_t n, double* factor, double* ortho, double* colratio,
+                  void* ws, size_t ws_bytes, rnr_stream_t stream);
 
 #ifdef __cplusplus
 }

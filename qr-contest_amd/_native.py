@@ -45,6 +45,8 @@ SIGNATURES = {
     "rnr_frame_f32_workspace": (_int, [_i64, _i64, _szp]),
     "rnr_frame_f32": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
     "rnr_chart_f32": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "rnr_check_f64_workspace": (_int, [_i64, _i64, _szp]),
+    "rnr_check_f64": (_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
 }
 
 
@@ -94,8 +96,8 @@ def check(fn: str, status: int) -> None:
 
 
 def workspace_bytes(kind: str, batch: int, n: int) -> int:
-    """Workspace size for one of "qr", "lu", "cholqr", "frame"."""
+    """Workspace size for one of "qr", "lu", "cholqr", "frame", "check"."""
     out = ctypes.c_size_t(0)
-    name = f"rnr_{kind}_f32_workspace"
+    name = "rnr_check_f64_workspace" if kind == "check" else f"rnr_{kind}_f32_workspace"
     check(name, getattr(lib(), name)(int(batch), int(n), ctypes.byref(out)))
     return int(out.value)

@@ -96,6 +96,16 @@ def test_argument_validation_before_any_launch(native, lib):
     assert lib.rnr_chart_f32(None, 2, 8, fake, fake, None) == native.RNR_ERR_INVALID_ARG
     assert lib.rnr_lu_f32(fake, 2, 8, 64, fake, None, fake, 1 << 30, None) == native.RNR_ERR_INVALID_ARG
     assert lib.rnr_cholqr_f32(fake, 2, 8, 64, None, None, None, fake, 1 << 30, None) == native.RNR_ERR_INVALID_ARG
+    # the GPU gate checker
+    c = lib.rnr_check_f64
+    cneed = native.workspace_bytes("check", 2, 16)
+    assert cneed > 0
+    assert c(None, 256, fake, fake, 2, 16, fake, fake, None, fake, cneed, None) == native.RNR_ERR_INVALID_ARG
+    assert c(fake, 255, fake, fake, 2, 16, fake, fake, None, fake, cneed, None) == native.RNR_ERR_INVALID_ARG
+    assert c(fake, 256, fake, fake, 2, 0, fake, fake, None, fake, cneed, None) == native.RNR_ERR_UNSUPPORTED_N
+    assert c(fake, 256, fake, fake, 2, 16, fake, fake, None, fake, cneed - 1, None) == native.RNR_ERR_WORKSPACE
+    assert c(fake, 256, fake, fake, 2, 16, fake, fake, None, fake + 8, cneed, None) == native.RNR_ERR_MISALIGNED
+    assert c(None, 256, None, None, 0, 16, None, None, None, None, 0, None) == native.RNR_OK
 
 
 def test_python_layer_rejects_cpu_and_non_square(pkg):
