@@ -42,6 +42,7 @@ __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
   constexpr int PER = BK * BM / 256;  // elements per thread per operand per chunk
   __shared__ __attribute__((aligned(16))) float Xs[2][BK][BM];
   __shared__ __attribute__((aligned(16))) float Ys[2][BK][BM];
+  __shared__ int lps[RNR_MAX_N];  // the row map of L (L view only)
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5;
@@ -61,7 +62,15 @@ __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
     for (int nj = 0; nj < NB; ++nj) acc[mi][nj] = zero16();
 
   float rx[PER], ry[PER];
-  const int* lp = a.lperm ? a.lperm + (int64_t)b * n : nullptr;
+  // the row map is staged in LDS once: every K chunk then looks its rows up there instead of
+  // waiting on a dependent global load before the data load
+  const int* lp = nullptr;
+  if (a.lperm) {
+    const int* g = a.lperm + (int64_t)b * n;
+    for (int i = (a.klo_from_j ? j0 : 0) + tid; i < n; i += 256) lps[i] = g[i];
+    __syncthreads();
+    lp = lps;
+  }
   // element (r, c) of the unit-lower view: below the diagonal from row lp[r], 1 on it, 0 above
   auto lview4 = [&](int gr, int c) -> float4 {
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
