@@ -22,6 +22,8 @@
  *   rnr_lu_f32      torch.linalg.lu(A) (P, L; U dropped) reflection_no_reflectors.py:66
  *   rnr_cholqr_f32  _cholqr(M) -> M R^-1                 reflection_no_reflectors.py:68-77
  *   rnr_chart_f32   _chart(Q) -> (Y, s), tau recompute   reflection_no_reflectors.py:86-176,192
+ *   rnr_orgqr_f32   torch.linalg.householder_product    README.md:122-128 (the consumer)
+ *   rnr_ormqr_f32   torch.ormqr (left)                  README.md:122-128
  *   rnr_check_f64   check / check_percol (fp64 gates)    common/oracle.py:152-195
  */
 #ifndef RNRQR_H
@@ -110,6 +112,17 @@ int rnr_frame_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride
  * signs (+1/-1) and tau = 2 / (1 + sum_{i>k} Y[i][k]^2).  No workspace. */
 int rnr_chart_f32(float* Y, int64_t batch, int64_t n, float* s, float* tau,
                   rnr_stream_t stream);
+
+/* ---- consumers of the path's output (README.md:122-128) ------------------------------
+ * Q = householder_product(H, tau) (torch.linalg.householder_product), batch x n x n, all
+ * contiguous. */
+int rnr_orgqr_f32(const float* H, const float* tau, int64_t batch, int64_t n, float* Q,
+                  rnr_stream_t stream);
+
+/* C <- Q C (transpose == 0) or Q^T C (transpose != 0) in place (torch.ormqr, left side):
+ * C is batch x n x ncol with row stride ldc >= ncol and batch stride >= n * ldc. */
+int rnr_ormqr_f32(const float* H, const float* tau, int64_t batch, int64_t n, float* C, int64_t ncol,
+                  int64_t ldc, int64_t batch_stride_c, int transpose, rnr_stream_t stream);
 
 /* ---- consumer of the path's output: the contest gates, evaluated on the GPU -------------
  * fp64 restatement of the reference checker (common/oracle.py:152-195, check and

@@ -45,6 +45,8 @@ SIGNATURES = {
     "rnr_frame_f32_workspace": (_int, [_i64, _i64, _szp]),
     "rnr_frame_f32": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
     "rnr_chart_f32": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "rnr_orgqr_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "rnr_ormqr_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _int, _vp]),
     "rnr_check_f64_workspace": (_int, [_i64, _i64, _szp]),
     "rnr_check_f64": (_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
 }

@@ -7,111 +7,16 @@
 //   colratio = max_j ||(triu(H) - Q^T A)[:, j]||_1 / (20 n eps32 ||A[:, j]||_1)   (:171-195)
 //
 // with the matrix 1-norm (largest absolute column sum).  Three kernels, all float64:
-//   k_formq   Q = H_0 H_1 ... H_{n-1} I by blocked WY accumulation: panels of PB reflectors,
-//             last panel first, P = I - V T V^T with T from the compact-WY recurrence
-//             (LAPACK dlarft, forward / columnwise); one matrix per 512-thread workgroup, one
-//             column of Q per thread, V and T in LDS;
+//   k_apply_q Q = H_0 H_1 ... H_{n-1} I in float64 by blocked WY accumulation (applyq.hpp);
 //   k_chk_tn  C = Q^T X for X = A (widened) or Q, 64 x 64 tiles, K staged through LDS; the
 //             epilogue reduces |C - ref| (ref = triu(H) or I) over the tile's 64 rows into
 //             per-(row tile, column) partial sums -- no atomics, so the result is repeatable;
 //   k_chk_red per matrix: column sums of the partials and of |A|, then the three maxima.
 #include "../../include/rnrqr.h"
-#include "common.hpp"
+#include "applyq.hpp"
 
 namespace rnr {
 namespace {
-
-constexpr int kFqThreads = 512;
-
-struct FormQArgs {
-  const float* H;
-  const float* tau;
-  double* Q;
-  int n;
-};
-
-template <int PB>
-__global__ __launch_bounds__(kFqThreads) void k_formq(FormQArgs a) {
-  extern __shared__ __attribute__((aligned(16))) double smd[];
-  const int n = a.n, b = blockIdx.x, tid = threadIdx.x;
-  const float* H = a.H + (int64_t)b * n * n;
-  const float* tau = a.tau + (int64_t)b * n;
-  double* Q = a.Q + (int64_t)b * n * n;
-  double* V = smd;                       // [m][PB]: row k0 + r of reflector k0 + j
-  double* T = V + (size_t)n * PB;        // [PB][PB] upper triangular
-  double* S = T + PB * PB;               // [PB][PB] V^T V (strict upper part)
-
-  for (int64_t idx = tid; idx < (int64_t)n * n; idx += kFqThreads) {
-    const int i = (int)(idx / n), c = (int)(idx - (int64_t)i * n);
-    Q[idx] = (i == c) ? 1.0 : 0.0;
-  }
-  __syncthreads();
-
-  const int np = (n + PB - 1) / PB;
-  for (int p = np - 1; p >= 0; --p) {
-    const int k0 = p * PB, kb = min(PB, n - k0), m = n - k0;
-    // reflector v_j = e_j (in panel coordinates) + H[k0 + j + 1 :, k0 + j]
-    for (int idx = tid; idx < m * PB; idx += kFqThreads) {
-      const int r = idx / PB, j = idx - r * PB;
-      double v = 0.0;
-      if (j < kb) v = (r < j) ? 0.0 : (r == j ? 1.0 : (double)H[(int64_t)(k0 + r) * n + k0 + j]);
-      V[idx] = v;
-    }
-    __syncthreads();
-    if (tid < PB * PB) {
-      const int i = tid / PB, j = tid - i * PB;
-      double acc = 0.0;
-      if (i < j && j < kb)
-        for (int r = j; r < m; ++r) acc += V[r * PB + i] * V[r * PB + j];
-      S[tid] = acc;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      // T[j][j] = tau_j;  T[0:j, j] = -tau_j T[0:j, 0:j] (V^T v_j)[0:j]
-      for (int j = 0; j < PB; ++j) {
-        const double tj = (j < kb) ? (double)tau[k0 + j] : 0.0;
-        for (int i = 0; i < j; ++i) {
-          double acc = 0.0;
-          for (int l = i; l < j; ++l) acc += T[i * PB + l] * S[l * PB + j];
-          T[i * PB + j] = -tj * acc;
-        }
-        T[j * PB + j] = tj;
-        for (int i = j + 1; i < PB; ++i) T[i * PB + j] = 0.0;
-      }
-    }
-    __syncthreads();
-    // Q[k0:, c] -= V T (V^T Q[k0:, c]) for the columns c >= k0 (columns left of k0 are still
-    // unit vectors that this panel does not touch)
-    for (int c = k0 + tid; c < n; c += kFqThreads) {
-      double z[PB];
-#pragma unroll
-      for (int j = 0; j < PB; ++j) z[j] = 0.0;
-      for (int r = 0; r < m; ++r) {
-        const double y = Q[(int64_t)(k0 + r) * n + c];
-#pragma unroll
-        for (int j = 0; j < PB; ++j) z[j] += V[r * PB + j] * y;
-      }
-      double w[PB];
-#pragma unroll
-      for (int i = 0; i < PB; ++i) {
-        double acc = 0.0;
-#pragma unroll
-        for (int j = i; j < PB; ++j) acc += T[i * PB + j] * z[j];
-        w[i] = acc;
-      }
-      for (int r = 0; r < m; ++r) {
-        double y = Q[(int64_t)(k0 + r) * n + c];
-#pragma unroll
-        for (int j = 0; j < PB; ++j) y -= V[r * PB + j] * w[j];
-        Q[(int64_t)(k0 + r) * n + c] = y;
-      }
-    }
-    __syncthreads();
-  }
-}
-
-template <int PB>
-size_t formq_lds(int n) { return sizeof(double) * ((size_t)n * PB + 2 * PB * PB); }
 
 struct TnArgs64 {
   const double* Q;     // [batch][n][n]
@@ -276,19 +181,19 @@ int rnr_check_f64(const float* A, int64_t batch_stride, const float* H, const fl
   double* pe = reinterpret_cast<double*>(base + up256((size_t)batch * n * n * sizeof(double)));
   double* po = reinterpret_cast<double*>(reinterpret_cast<char*>(pe) + up256((size_t)batch * nt * n * sizeof(double)));
 
-  FormQArgs fq{H, tau, Q, ni};
+  ApplyQArgs<double> fq{H, tau, Q, (int64_t)n * n, ni, ni, ni};
   if (ni <= 1024) {
-    const size_t lds = formq_lds<16>(ni);
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_formq<16>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess)
+    const size_t lds = applyq_lds<double, 16>(ni);
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_apply_q<double, 16, false, true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
       return RNR_ERR_HIP;
-    k_formq<16><<<dim3((unsigned)batch), dim3(kFqThreads), lds, st>>>(fq);
+    k_apply_q<double, 16, false, true><<<dim3((unsigned)batch), dim3(kApplyQThreads), lds, st>>>(fq);
   } else {
-    const size_t lds = formq_lds<8>(ni);
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_formq<8>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess)
+    const size_t lds = applyq_lds<double, 8>(ni);
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_apply_q<double, 8, false, true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
       return RNR_ERR_HIP;
-    k_formq<8><<<dim3((unsigned)batch), dim3(kFqThreads), lds, st>>>(fq);
+    k_apply_q<double, 8, false, true><<<dim3((unsigned)batch), dim3(kApplyQThreads), lds, st>>>(fq);
   }
   if (hipGetLastError() != hipSuccess) return RNR_ERR_HIP;
 

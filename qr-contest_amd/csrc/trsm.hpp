@@ -51,12 +51,14 @@ struct WblkArgs {
 
 // W[:c, c] = R[:c, c] Dinv_c for block column c >= 1 (64-wide blocks): one block column of
 // one matrix per 256-thread workgroup.  Dinv_c is staged in LDS once; each wave takes 32-row
-// strips of the rows above the diagonal block (two 32x32 accumulators over the 64 columns,
-// K = 64 on v_mfma_f32_32x32x2f32), so every R entry is read from HBM once.  The K order
-// inside the product is permuted so that a lane reads R with float4 loads: at step t lane
-// (l32, h) takes k = 8 (t / 4) + 4 h + t % 4 from both operands.
+// strips of the rows above the diagonal block: the strip is read row-contiguously (16 lanes
+// per 64-float row, float4 each) into the wave's own LDS tile, then multiplied on
+// v_mfma_f32_32x32x2f32 (two 32x32 accumulators over the 64 columns, K = 64), so every R entry
+// is read from HBM once and coalesced.
 __global__ __launch_bounds__(256) void k_wblocks(WblkArgs a) {
+  constexpr int LDR = 65;  // odd stride: the MFMA operand reads (32 rows, one column) are conflict-free
   __shared__ __attribute__((aligned(16))) float Ds[64 * 64];
+  __shared__ float Rs[4][32 * LDR];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5;
   const int pid = xcd_remap(blockIdx.x, a.total);
@@ -64,6 +66,7 @@ __global__ __launch_bounds__(256) void k_wblocks(WblkArgs a) {
   const float* R = a.R + b * a.sr;
   const float* Dv = a.Dinv + (int64_t)b * n * 64;
   float* W = a.Wm + b * a.sw;
+  float* Rw = Rs[wid];
   for (int idx = tid; idx < 64 * 16; idx += 256) {
     const int k = idx >> 4, j4 = idx & 15;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -72,29 +75,33 @@ __global__ __launch_bounds__(256) void k_wblocks(WblkArgs a) {
   }
   __syncthreads();
   for (int strip = wid; strip < 2 * c; strip += 4) {
-    const int row = 32 * strip + l32;  // < c0 <= n
-    float4 av[8];
+    // strip rows 32 strip .. +31 (< c0 <= n), columns c0 .. c0 + 63: 4 rows per instruction
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const int k = c0 + 8 * v + 4 * h;
-      if (a.vec4 && k + 3 < n) {
-        av[v] = *reinterpret_cast<const float4*>(R + (int64_t)row * n + k);
+    for (int u = 0; u < 8; ++u) {
+      const int rr = 4 * u + (lane >> 4), col = c0 + 4 * (lane & 15);
+      const float* src = R + (int64_t)(32 * strip + rr) * n + col;
+      float4 v;
+      if (a.vec4 && col + 3 < n) {
+        v = *reinterpret_cast<const float4*>(src);
       } else {
-        av[v].x = (k < n) ? R[(int64_t)row * n + k] : 0.f;
-        av[v].y = (k + 1 < n) ? R[(int64_t)row * n + k + 1] : 0.f;
-        av[v].z = (k + 2 < n) ? R[(int64_t)row * n + k + 2] : 0.f;
-        av[v].w = (k + 3 < n) ? R[(int64_t)row * n + k + 3] : 0.f;
+        v.x = (col < n) ? src[0] : 0.f;
+        v.y = (col + 1 < n) ? src[1] : 0.f;
+        v.z = (col + 2 < n) ? src[2] : 0.f;
+        v.w = (col + 3 < n) ? src[3] : 0.f;
       }
+      float* d = Rw + rr * LDR + 4 * (lane & 15);
+      d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
     }
+    wave_lds_order();
     f32x16 acc0 = zero16(), acc1 = zero16();
 #pragma unroll
     for (int t = 0; t < 32; ++t) {
-      const int kk = 8 * (t >> 2) + 4 * h + (t & 3);
-      const float4 v4 = av[t >> 2];
-      const float x = (t & 3) == 0 ? v4.x : (t & 3) == 1 ? v4.y : (t & 3) == 2 ? v4.z : v4.w;
-      acc0 = mfma(x, Ds[kk * 64 + l32], acc0);
-      acc1 = mfma(x, Ds[kk * 64 + 32 + l32], acc1);
+      const int k = 2 * t + h;
+      const float x = Rw[l32 * LDR + k];
+      acc0 = mfma(x, Ds[k * 64 + l32], acc0);
+      acc1 = mfma(x, Ds[k * 64 + 32 + l32], acc1);
     }
+    wave_lds_order();  // the next strip's tile stores stay behind these reads
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int64_t o = (int64_t)(32 * strip + acc_row(r, lane)) * n + c0 + l32;
