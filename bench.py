@@ -115,6 +115,10 @@ def main() -> None:
     ap.add_argument("--config", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-geqrf", action="store_true")
+    ap.add_argument("--no-gates", action="store_true",
+                    help="skip the float64 gate check of the output (profiling runs)")
+    ap.add_argument("--no-aux", action="store_true",
+                    help="skip the generator and Q-consumer timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB device copy three times (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -143,8 +147,13 @@ def main() -> None:
         torch.cuda.synchronize()
         del x, y
 
+    t_gen = time.perf_counter()
     A_cpu = wl.make_batch(args.config)
+    host_gen_ms = (time.perf_counter() - t_gen) * 1e3
+    t_h2d = time.perf_counter()
     A = A_cpu.to(dev)
+    torch.cuda.synchronize()
+    h2d_ms = (time.perf_counter() - t_h2d) * 1e3
     plan = rnr.QRPlan(cfg.batch, cfg.n, dev)
     stream = torch.cuda.current_stream(dev)
 
@@ -162,15 +171,44 @@ def main() -> None:
 
     # validity of what was timed: the contest gates on every matrix of the last step's output,
     # evaluated in float64 on the GPU (rnr_check_f64), outside the timed region
-    chk = importlib.import_module("qr-contest_amd.check")
-    torch.cuda.synchronize()
-    t_chk = time.perf_counter()
-    fr, og, ft, ot, ok = chk.check(A, plan.H, plan.tau)
-    ratio, _, ok_col = chk.check_percol(A, plan.H, plan.tau)
-    torch.cuda.synchronize()
-    chk_ms = (time.perf_counter() - t_chk) * 1e3
-    n_checked = cfg.batch
-    info_ok = int(plan.info.abs().sum().item()) == 0
+    gates = None
+    if not args.no_gates:
+        chk = importlib.import_module("qr-contest_amd.check")
+        torch.cuda.synchronize()
+        t_chk = time.perf_counter()
+        fr, og, ft, ot, ok = chk.check(A, plan.H, plan.tau)
+        ratio, _, ok_col = chk.check_percol(A, plan.H, plan.tau)
+        torch.cuda.synchronize()
+        chk_ms = (time.perf_counter() - t_chk) * 1e3
+        info_ok = int(plan.info.abs().sum().item()) == 0
+        gates = {"factor_max": fr, "factor_gate": ft, "ortho_max": og, "ortho_gate": ot,
+                 "percol_max": ratio, "checked": cfg.batch, "checker": "rnr_check_f64 (GPU, float64)",
+                 "checker_ms": chk_ms, "pass": bool(ok.all()) and bool(ok_col.all()) and info_ok}
+
+    # the steps either side of the path: the input generators and the Q consumers
+    aux = None
+    if not args.no_aux:
+        gen = importlib.import_module("qr-contest_amd.generate")
+        hh = importlib.import_module("qr-contest_amd.householder")
+        gen.device_batch(args.config, device=dev)
+        torch.cuda.synchronize()
+        t_dg = time.perf_counter()
+        gen.device_batch(args.config, device=dev)
+        torch.cuda.synchronize()
+        dev_gen_ms = (time.perf_counter() - t_dg) * 1e3
+        Hc, tc = plan.H.clone(), plan.tau.clone()
+        hh.householder_product(Hc, tc)
+        torch.cuda.synchronize()
+        orgqr_ms = _events_ms(lambda: hh.householder_product(Hc, tc), 3, stream)
+        C = torch.randn(cfg.batch, cfg.n, 64, device=dev)
+        hh.ormqr(Hc, tc, C, transpose=True)
+        torch.cuda.synchronize()
+        ormqr_ms = _events_ms(lambda: hh.ormqr(Hc, tc, C, transpose=True), 3, stream)
+        aux = {"generator": {"device_ms": dev_gen_ms, "host_ms": host_gen_ms, "host_to_device_ms": h2d_ms,
+                             "device_source": "rnr_generate_f32 (Philox4x32-10, float64 Haar factors)",
+                             "host_source": "workloads.make_batch (torch CPU, float64)"},
+               "orgqr": {"ms_per_batch": orgqr_ms, "matrices_per_s": cfg.batch / (orgqr_ms / 1e3)},
+               "ormqr_qt_64cols": {"ms_per_batch": ormqr_ms}}
 
     # per-kernel times of the live path: rnr_qr_f32_timed records an event before each launch
     lib = native.lib()
@@ -252,9 +290,8 @@ def main() -> None:
         },
         "stages_ms": stage_ms,
         "kernels": per_kernel,
-        "gates": {"factor_max": fr, "factor_gate": ft, "ortho_max": og, "ortho_gate": ot,
-                  "percol_max": ratio, "checked": n_checked, "checker": "rnr_check_f64 (GPU, float64)",
-                  "checker_ms": chk_ms, "pass": bool(ok.all()) and bool(ok_col.all()) and info_ok},
+        "gates": gates,
+        "aux": aux,
         "gpu_torch_geqrf": gpu_geqrf,
         "cpu_baseline": cpu,
     }

@@ -22,6 +22,7 @@
  *   rnr_lu_f32      torch.linalg.lu(A) (P, L; U dropped) reflection_no_reflectors.py:66
  *   rnr_cholqr_f32  _cholqr(M) -> M R^-1                 reflection_no_reflectors.py:68-77
  *   rnr_chart_f32   _chart(Q) -> (Y, s), tau recompute   reflection_no_reflectors.py:86-176,192
+ *   rnr_generate_f32  make_batch / gen_* (the input step)   common/oracle.py:43-146
  *   rnr_orgqr_f32   torch.linalg.householder_product    README.md:122-128 (the consumer)
  *   rnr_ormqr_f32   torch.ormqr (left)                  README.md:122-128
  *   rnr_check_f64   check / check_percol (fp64 gates)    common/oracle.py:152-195
@@ -112,6 +113,15 @@ int rnr_frame_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride
  * signs (+1/-1) and tau = 2 / (1 + sum_{i>k} Y[i][k]^2).  No workspace. */
 int rnr_chart_f32(float* Y, int64_t batch, int64_t n, float* s, float* tau,
                   rnr_stream_t stream);
+
+/* ---- the input step: device-side seeded generators (common/oracle.py:43-146) ------------
+ * The batch of benchmark configuration `config` (1..5; classes as in qr-contest_amd/workloads.py)
+ * with its own Philox4x32-10 streams keyed by `seed`: matrix i depends only on (config, n, seed,
+ * i), not on the batch size.  A is batch x n x n float32, contiguous.  The workspace (float64
+ * Haar factors) is 0 bytes when the configuration has no Haar-class matrix in the batch. */
+int rnr_generate_workspace(int config, int64_t batch, int64_t n, size_t* bytes);
+int rnr_generate_f32(int config, int64_t batch, int64_t n, uint64_t seed, float* A, void* workspace,
+                     size_t workspace_bytes, rnr_stream_t stream);
 
 /* ---- consumers of the path's output (README.md:122-128) ------------------------------
  * Q = householder_product(H, tau) (torch.linalg.householder_product), batch x n x n, all

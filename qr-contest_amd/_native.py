@@ -27,6 +27,7 @@ QR_STAGES = ("lu", "gram_L", "chol_1", "trsm_1", "gram_Q1", "chol_2", "trsm_2", 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
+_u64 = ctypes.c_uint64
 _szp = ctypes.POINTER(ctypes.c_size_t)
 _int = ctypes.c_int
 
@@ -45,6 +46,8 @@ SIGNATURES = {
     "rnr_frame_f32_workspace": (_int, [_i64, _i64, _szp]),
     "rnr_frame_f32": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
     "rnr_chart_f32": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "rnr_generate_workspace": (_int, [_int, _i64, _i64, _szp]),
+    "rnr_generate_f32": (_int, [_int, _i64, _i64, _u64, _vp, _vp, _sz, _vp]),
     "rnr_orgqr_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "rnr_ormqr_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _int, _vp]),
     "rnr_check_f64_workspace": (_int, [_i64, _i64, _szp]),

@@ -6,9 +6,13 @@
 // from the compact-WY recurrence (LAPACK dlarft, forward / columnwise):
 // T[j][j] = tau_j, T[0:j, j] = -tau_j T[0:j, 0:j] (V^T v_j)[0:j].  op = Q applies the panels
 // last first (Y <- P Y), op = Q^T first to last (Y <- P^T Y = Y - V T^T V^T Y).  One matrix per
-// 512-thread workgroup, one column of Y per thread, V / T in LDS; only rows >= k0 change.
+// 512-thread workgroup and 512-column chunk (grid (batch, ceil(nc / 512))), one column of Y per
+// thread, V / T in LDS; only rows >= k0 change.  Columns are independent, so the chunks of one
+// matrix need no communication (each rebuilds the panel's T).
 // IDENT: Y starts as the identity (orgqr), and then a panel leaves the columns left of k0
 // untouched (they are still unit vectors).
+// T is the arithmetic type, TH the storage type of the reflectors (float for this library's
+// output, double for the generator's Haar factors).
 #pragma once
 #include "common.hpp"
 
@@ -16,10 +20,10 @@ namespace rnr {
 
 constexpr int kApplyQThreads = 512;
 
-template <typename T>
+template <typename T, typename TH = float>
 struct ApplyQArgs {
-  const float* H;    // [batch][n][n]
-  const float* tau;  // [batch][n]
+  const TH* H;       // [batch][n][n]
+  const TH* tau;     // [batch][n]
   T* Y;              // [batch] x n rows x nc columns, row stride ldy, batch stride sy
   int64_t sy;
   int ldy;
@@ -29,25 +33,25 @@ struct ApplyQArgs {
 template <typename T, int PB>
 inline size_t applyq_lds(int n) { return sizeof(T) * ((size_t)n * PB + 2 * PB * PB); }
 
-template <typename T, int PB, bool TRANS, bool IDENT>
-__global__ __launch_bounds__(kApplyQThreads) void k_apply_q(ApplyQArgs<T> a) {
+inline dim3 applyq_grid(int64_t batch, int nc) {
+  return dim3((unsigned)batch, (unsigned)((nc + kApplyQThreads - 1) / kApplyQThreads));
+}
+
+template <typename T, int PB, bool TRANS, bool IDENT, typename TH = float>
+__global__ __launch_bounds__(kApplyQThreads) void k_apply_q(ApplyQArgs<T, TH> a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smraw[];
   T* V = reinterpret_cast<T*>(smraw);  // [m][PB]: row k0 + r of reflector k0 + j
   const int n = a.n, nc = a.nc, b = blockIdx.x, tid = threadIdx.x;
   T* Tm = V + (size_t)n * PB;          // [PB][PB] upper triangular
   T* S = Tm + PB * PB;                 // [PB][PB] V^T V (strict upper part)
-  const float* H = a.H + (int64_t)b * n * n;
-  const float* tau = a.tau + (int64_t)b * n;
+  const TH* H = a.H + (int64_t)b * n * n;
+  const TH* tau = a.tau + (int64_t)b * n;
   T* Y = a.Y + b * a.sy;
   const int ld = a.ldy;
+  const int c = blockIdx.y * kApplyQThreads + tid;  // this thread's column
 
-  if (IDENT) {
-    for (int64_t idx = tid; idx < (int64_t)n * nc; idx += kApplyQThreads) {
-      const int i = (int)(idx / nc), c = (int)(idx - (int64_t)i * nc);
-      Y[(int64_t)i * ld + c] = (i == c) ? T(1) : T(0);
-    }
-    __syncthreads();
-  }
+  if (IDENT && c < nc)
+    for (int i = 0; i < n; ++i) Y[(int64_t)i * ld + c] = (i == c) ? T(1) : T(0);
 
   const int np = (n + PB - 1) / PB;
   for (int s = 0; s < np; ++s) {
@@ -81,7 +85,7 @@ __global__ __launch_bounds__(kApplyQThreads) void k_apply_q(ApplyQArgs<T> a) {
       }
     }
     __syncthreads();
-    for (int c = (IDENT ? k0 : 0) + tid; c < nc; c += kApplyQThreads) {
+    if (c < nc && (!IDENT || c >= k0)) {
       T z[PB];
 #pragma unroll
       for (int j = 0; j < PB; ++j) z[j] = T(0);

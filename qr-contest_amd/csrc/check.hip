@@ -187,13 +187,13 @@ int rnr_check_f64(const float* A, int64_t batch_stride, const float* H, const fl
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_apply_q<double, 16, false, true>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
       return RNR_ERR_HIP;
-    k_apply_q<double, 16, false, true><<<dim3((unsigned)batch), dim3(kApplyQThreads), lds, st>>>(fq);
+    k_apply_q<double, 16, false, true><<<applyq_grid(batch, ni), dim3(kApplyQThreads), lds, st>>>(fq);
   } else {
     const size_t lds = applyq_lds<double, 8>(ni);
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_apply_q<double, 8, false, true>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
       return RNR_ERR_HIP;
-    k_apply_q<double, 8, false, true><<<dim3((unsigned)batch), dim3(kApplyQThreads), lds, st>>>(fq);
+    k_apply_q<double, 8, false, true><<<applyq_grid(batch, ni), dim3(kApplyQThreads), lds, st>>>(fq);
   }
   if (hipGetLastError() != hipSuccess) return RNR_ERR_HIP;
 

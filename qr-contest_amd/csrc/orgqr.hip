@@ -15,7 +15,7 @@ int launch_apply(const ApplyQArgs<float>& a, int64_t batch, hipStream_t st) {
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_apply_q<float, 16, TRANS, IDENT>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return RNR_ERR_HIP;
-  k_apply_q<float, 16, TRANS, IDENT><<<dim3((unsigned)batch), dim3(kApplyQThreads), lds, st>>>(a);
+  k_apply_q<float, 16, TRANS, IDENT><<<applyq_grid(batch, a.nc), dim3(kApplyQThreads), lds, st>>>(a);
   return hipGetLastError() == hipSuccess ? RNR_OK : RNR_ERR_HIP;
 }
 

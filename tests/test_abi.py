@@ -106,6 +106,20 @@ def test_argument_validation_before_any_launch(native, lib):
     assert c(fake, 256, fake, fake, 2, 16, fake, fake, None, fake, cneed - 1, None) == native.RNR_ERR_WORKSPACE
     assert c(fake, 256, fake, fake, 2, 16, fake, fake, None, fake + 8, cneed, None) == native.RNR_ERR_MISALIGNED
     assert c(None, 256, None, None, 0, 16, None, None, None, None, 0, None) == native.RNR_OK
+    # the device generators
+    gw = ctypes.c_size_t(0)
+    assert lib.rnr_generate_workspace(4, 256, 512, ctypes.byref(gw)) == native.RNR_OK
+    assert gw.value >= 128 * 3 * 512 * 512 * 8          # 128 Haar matrices: U, W and Y in float64
+    assert lib.rnr_generate_workspace(1, 16, 64, ctypes.byref(gw)) == native.RNR_OK and gw.value == 0
+    assert lib.rnr_generate_workspace(4, 1, 64, ctypes.byref(gw)) == native.RNR_OK and gw.value == 0
+    assert lib.rnr_generate_workspace(0, 1, 64, ctypes.byref(gw)) == native.RNR_ERR_INVALID_ARG
+    gn = lib.rnr_generate_f32
+    assert gn(6, 2, 16, 0, fake, None, 0, None) == native.RNR_ERR_INVALID_ARG
+    assert gn(4, 2, 0, 0, fake, None, 0, None) == native.RNR_ERR_UNSUPPORTED_N
+    assert gn(4, 2, 16, 0, None, None, 0, None) == native.RNR_ERR_INVALID_ARG
+    assert gn(4, 2, 16, 0, fake, None, 0, None) == native.RNR_ERR_WORKSPACE   # matrix 1 is Haar
+    assert gn(4, 2, 16, 0, fake, fake + 8, 1 << 30, None) == native.RNR_ERR_MISALIGNED
+    assert gn(4, 0, 16, 0, None, None, 0, None) == native.RNR_OK
     # the Q consumers
     o = lib.rnr_orgqr_f32
     assert o(None, fake, 2, 16, fake, None) == native.RNR_ERR_INVALID_ARG
