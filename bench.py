@@ -204,7 +204,14 @@ def main() -> None:
         hh.ormqr(Hc, tc, C, transpose=True)
         torch.cuda.synchronize()
         ormqr_ms = _events_ms(lambda: hh.ormqr(Hc, tc, C, transpose=True), 3, stream)
-        aux = {"generator": {"device_ms": dev_gen_ms, "host_ms": host_gen_ms, "host_to_device_ms": h2d_ms,
+        cmpm = importlib.import_module("qr-contest_amd.comparator")
+        cmpm.hh_geqrf(A)
+        torch.cuda.synchronize()
+        hh_ms = _events_ms(lambda: cmpm.hh_geqrf(A), 3, stream)
+        aux = {"householder_comparator": {"ms_per_batch": hh_ms, "matrices_per_s": cfg.batch / (hh_ms / 1e3),
+                                          "source": "rnr_hh_geqrf_f32 (blocked Householder, geqrf layout; "
+                                                    "benchmark only, not the product path)"},
+               "generator": {"device_ms": dev_gen_ms, "host_ms": host_gen_ms, "host_to_device_ms": h2d_ms,
                              "device_source": "rnr_generate_f32 (Philox4x32-10, float64 Haar factors)",
                              "host_source": "workloads.make_batch (torch CPU, float64)"},
                "orgqr": {"ms_per_batch": orgqr_ms, "matrices_per_s": cfg.batch / (orgqr_ms / 1e3)},

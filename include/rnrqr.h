@@ -26,6 +26,7 @@
  *   rnr_orgqr_f32   torch.linalg.householder_product    README.md:122-128 (the consumer)
  *   rnr_ormqr_f32   torch.ormqr (left)                  README.md:122-128
  *   rnr_check_f64   check / check_percol (fp64 gates)    common/oracle.py:152-195
+ *   rnr_hh_geqrf_f32  blocked Householder (comparator only)  householder/submission_routed_v3.py:225-281
  */
 #ifndef RNRQR_H
 #define RNRQR_H
@@ -133,6 +134,14 @@ int rnr_orgqr_f32(const float* H, const float* tau, int64_t batch, int64_t n, fl
  * C is batch x n x ncol with row stride ldc >= ncol and batch stride >= n * ldc. */
 int rnr_ormqr_f32(const float* H, const float* tau, int64_t batch, int64_t n, float* C, int64_t ncol,
                   int64_t ldc, int64_t batch_stride_c, int transpose, rnr_stream_t stream);
+
+/* ---- benchmark comparator (NOT on the reflector-free path) --------------------------------
+ * Householder blocked-WY QR in torch.geqrf layout, in place on H (A in, H out), float32: the
+ * classical route the reference measures its kernels against
+ * (householder/submission_routed_v3.py:225-281).  custom_kernel never calls it. */
+int rnr_hh_geqrf_workspace(int64_t batch, int64_t n, size_t* bytes);
+int rnr_hh_geqrf_f32(float* H, int64_t batch, int64_t n, float* tau, void* workspace, size_t workspace_bytes,
+                     rnr_stream_t stream);
 
 /* ---- consumer of the path's output: the contest gates, evaluated on the GPU -------------
  * fp64 restatement of the reference checker (common/oracle.py:152-195, check and

@@ -11,6 +11,8 @@ Modules
 ``checker``      the fp64 factor-residual / orthogonality gates of ``common/oracle.py:152-195``
 ``closed_form``  LAPACK ``geqrf`` plus the sign/tau post-map that the path equals in exact arithmetic
 ``textbook``     pure-Python unblocked getrf / potrf / trsm / chart for tiny matrices (brute force)
+``gen``          numpy restatement of the device generators (Philox4x32-10, Box-Muller, Stewart's
+                 Haar factors, the five configurations' classes)
 
 Pinning status (what checks each function; see ``tests/test_oracle.py``)
 -----------------------------------------------------------------------
@@ -21,6 +23,9 @@ Pinning status (what checks each function; see ``tests/test_oracle.py``)
 * ``rnr.custom_kernel`` -- geqrf(A) post-map (fp64, jitter 0: 1e-10; fp32: tolerance), special cases
   (upper-triangular, n = 1, zero matrix), the contest gates on all six pathology classes.
 * ``checker.check``   -- exact geqrf factors give ~1e-15; a planted 1 % error in R fails the gate.
+* ``gen``             -- Random123 Philox4x32-10 known-answer vectors; KS / moment tests of the streams;
+  Haar factors against numpy's sign-fixed QR of Gaussian matrices (two-sample KS, E tr Q = 0,
+  E (tr Q)^2 = 1); prescribed singular values by numpy SVD (``tests/test_oracle_gen.py``).
 The only part no check fixes to the last bit is the reference's exact fp32 rounding sequence inside
 torch.linalg (LAPACK); parity is therefore stated to an fp32 tolerance, not bitwise.
 """

@@ -48,6 +48,8 @@ SIGNATURES = {
     "rnr_chart_f32": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "rnr_generate_workspace": (_int, [_int, _i64, _i64, _szp]),
     "rnr_generate_f32": (_int, [_int, _i64, _i64, _u64, _vp, _vp, _sz, _vp]),
+    "rnr_hh_geqrf_workspace": (_int, [_i64, _i64, _szp]),
+    "rnr_hh_geqrf_f32": (_int, [_vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "rnr_orgqr_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "rnr_ormqr_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _int, _vp]),
     "rnr_check_f64_workspace": (_int, [_i64, _i64, _szp]),
@@ -101,8 +103,9 @@ def check(fn: str, status: int) -> None:
 
 
 def workspace_bytes(kind: str, batch: int, n: int) -> int:
-    """Workspace size for one of "qr", "lu", "cholqr", "frame", "check"."""
+    """Workspace size for one of "qr", "lu", "cholqr", "frame", "check", "hh_geqrf"."""
     out = ctypes.c_size_t(0)
-    name = "rnr_check_f64_workspace" if kind == "check" else f"rnr_{kind}_f32_workspace"
+    name = {"check": "rnr_check_f64_workspace", "hh_geqrf": "rnr_hh_geqrf_workspace"}.get(
+        kind, f"rnr_{kind}_f32_workspace")
     check(name, getattr(lib(), name)(int(batch), int(n), ctypes.byref(out)))
     return int(out.value)

@@ -120,6 +120,15 @@ def test_argument_validation_before_any_launch(native, lib):
     assert gn(4, 2, 16, 0, fake, None, 0, None) == native.RNR_ERR_WORKSPACE   # matrix 1 is Haar
     assert gn(4, 2, 16, 0, fake, fake + 8, 1 << 30, None) == native.RNR_ERR_MISALIGNED
     assert gn(4, 0, 16, 0, None, None, 0, None) == native.RNR_OK
+    # the Householder comparator
+    hw = ctypes.c_size_t(0)
+    assert lib.rnr_hh_geqrf_workspace(2, 100, ctypes.byref(hw)) == native.RNR_OK and hw.value == 2 * 32 * 32 * 4
+    hq = lib.rnr_hh_geqrf_f32
+    assert hq(None, 2, 16, fake, fake, hw.value, None) == native.RNR_ERR_INVALID_ARG
+    assert hq(fake, 2, 0, fake, fake, hw.value, None) == native.RNR_ERR_UNSUPPORTED_N
+    assert hq(fake, 2, 16, fake, fake, hw.value - 1, None) == native.RNR_ERR_WORKSPACE
+    assert hq(fake, 2, 16, fake, fake + 8, hw.value, None) == native.RNR_ERR_MISALIGNED
+    assert hq(None, 0, 16, None, None, 0, None) == native.RNR_OK
     # the Q consumers
     o = lib.rnr_orgqr_f32
     assert o(None, fake, 2, 16, fake, None) == native.RNR_ERR_INVALID_ARG
