@@ -153,6 +153,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
   const int n = a.n, b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5;
   const int lds_w = n > kCholNb ? n - kCholNb : 1;
+  // offsets inside one matrix are 32-bit (n * n < 2^31): one VGPR per address, not two
   float* G = a.G + b * a.sg;
   float* Dv = a.Dinv + (int64_t)b * n * 64;
 
@@ -181,8 +182,8 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
       // R_kk (upper) and Dinv_kk (row-major, zero below the diagonal) to HBM
       for (int idx = tid; idx < kb * 64; idx += kCholThreads) {
         const int i = idx >> 6, c = idx & 63;
-        if (c < kb && c >= i) G[(int64_t)(k0 + i) * n + k0 + c] = D[i * 65 + c];
-        Dv[(int64_t)(k0 + i) * 64 + c] = (c < kb) ? XT[c * 65 + i] : 0.f;
+        if (c < kb && c >= i) G[(k0 + i) * n + k0 + c] = D[i * 65 + c];
+        Dv[(k0 + i) * 64 + c] = (c < kb) ? XT[c * 65 + i] : 0.f;
       }
       if (w <= 0) break;  // uniform; kb == 64 below this line
 
@@ -190,11 +191,16 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
       // so it can overwrite them in G without racing other waves' reads.
       const int nch = (w + 31) >> 5;
       for (int job = wid; job < nch; job += NW) {
+        // lane-derived offsets are laundered per job: hoisted out of the block loop they
+        // would stay live across it (32+ VGPRs) and spill
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int l32 = ln & 31, h = ln >> 5;
         const int colr = job * 32 + l32, col = k1 + colr;
+        const int base = (k0 + h) * n + col;
         float bv[32];
 #pragma unroll
-        for (int t = 0; t < 32; ++t)
-          bv[t] = (col < n) ? G[(int64_t)(k0 + 2 * t + h) * n + col] : 0.f;
+        for (int t = 0; t < 32; ++t) bv[t] = (col < n) ? G[base + 2 * t * n] : 0.f;
         f32x16 acc0 = zero16(), acc1 = zero16();
 #pragma unroll
         for (int t = 0; t < 32; ++t) {
@@ -205,9 +211,9 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
         if (col < n) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int i0 = acc_row(r, lane), i1 = 32 + acc_row(r, lane);
-            G[(int64_t)(k0 + i0) * n + col] = acc0[r];
-            G[(int64_t)(k0 + i1) * n + col] = acc1[r];
+            const int i0 = acc_row(r, ln), i1 = 32 + acc_row(r, ln);
+            G[(k0 + i0) * n + col] = acc0[r];
+            G[(k0 + i1) * n + col] = acc1[r];
             if (a.strip_lds) {
               S[i0 * lds_w + colr] = acc0[r];
               S[i1 * lds_w + colr] = acc1[r];
@@ -227,6 +233,9 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
       for (int pr = t0; pr < npairs; pr += tstep) {
         int I, J;
         upper_tile(pr, nt, I, J);
+        int ln = lane;  // laundered per tile, as above
+        asm volatile("" : "+v"(ln));
+        const int l32 = ln & 31, h = ln >> 5;
         f32x16 acc[2][2];
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
@@ -234,9 +243,9 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
           for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const int row = k1 + I * 64 + mi * 32 + acc_row(r, lane);
+              const int row = k1 + I * 64 + mi * 32 + acc_row(r, ln);
               const int col = k1 + J * 64 + nj * 32 + l32;
-              acc[mi][nj][r] = (row < n && col < n) ? G[(int64_t)row * n + col] : 0.f;
+              acc[mi][nj][r] = (row < n && col < n) ? G[row * n + col] : 0.f;
             }
         if (!first) {
 #pragma unroll 4
@@ -250,8 +259,8 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
                 av[q] = (ci < w) ? -S[k * lds_w + ci] : 0.f;
                 bv[q] = (cj < w) ? S[k * lds_w + cj] : 0.f;
               } else {
-                av[q] = (ci < w) ? -G[(int64_t)(k0 + k) * n + k1 + ci] : 0.f;
-                bv[q] = (cj < w) ? G[(int64_t)(k0 + k) * n + k1 + cj] : 0.f;
+                av[q] = (ci < w) ? -G[(k0 + k) * n + k1 + ci] : 0.f;
+                bv[q] = (cj < w) ? G[(k0 + k) * n + k1 + cj] : 0.f;
               }
             }
 #pragma unroll
@@ -269,7 +278,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
             for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
               for (int r = 0; r < 16; ++r) {
-                const int i = mi * 32 + acc_row(r, lane), c = nj * 32 + l32;
+                const int i = mi * 32 + acc_row(r, ln), c = nj * 32 + l32;
                 D[i * 65 + c] = (i < kbn && c < kbn) ? acc[mi][nj][r] : (i == c ? 1.f : 0.f);
               }
           wave_lds_order();
@@ -284,9 +293,9 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
             for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
               for (int r = 0; r < 16; ++r) {
-                const int row = k1 + I * 64 + mi * 32 + acc_row(r, lane);
+                const int row = k1 + I * 64 + mi * 32 + acc_row(r, ln);
                 const int col = k1 + J * 64 + nj * 32 + l32;
-                if (row < n && col < n) G[(int64_t)row * n + col] = acc[mi][nj][r];
+                if (row < n && col < n) G[row * n + col] = acc[mi][nj][r];
               }
         }
       }
