@@ -39,6 +39,8 @@ struct LuArgs {
   int64_t sl;
   float* s;          // chart: signs, [batch][n]
   float* tau;        // chart: tau, [batch][n]
+  int k0;            // SPLIT: the panel this launch factors
+  float* X;          // SPLIT: out, L11^-1 of that panel, [batch][NB][NB]
 };
 
 constexpr int kLuThreads = 512;
@@ -61,7 +63,11 @@ inline size_t lu_lds_bytes(int n, int nb) {
   return sizeof(float) * (p + (size_t)nb * 64 + pl + 8 + 2 * 8 * (size_t)(nb + 4));
 }
 
-template <bool PIVOT, int NB, int RPT>
+// SPLIT = true: one launch factors only panel a.k0 and stops before its trailing update,
+// which k_lu_trail runs over many workgroups (for batches too small to fill the GPU with one
+// workgroup per matrix).  The row map then lives in a.perm between launches and L11^-1 goes
+// to a.X.
+template <bool PIVOT, int NB, int RPT, bool SPLIT = false>
 __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
   constexpr int T = kLuThreads, NW = T / 64;
   constexpr int NB4 = NB / 4;
@@ -84,12 +90,12 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
   auto sw = [](int r, int c) { return r * LDP + c; };
 
   if (PIVOT)
-    for (int i = tid; i < n; i += T) pl[i] = i;
+    for (int i = tid; i < n; i += T) pl[i] = (SPLIT && a.k0 > 0) ? a.perm[(int64_t)b * n + i] : i;
   if (tid < 3) pkeys[tid] = 0ull;
   int step = 0;  // LU column steps so far (selects the pivot key buffer)
   __syncthreads();
 
-  for (int k0 = 0; k0 < n; k0 += NB) {
+  for (int k0 = SPLIT ? a.k0 : 0; k0 < n; k0 += NB) {
     const int kb = min(NB, n - k0), m = n - k0, k1 = k0 + kb;
     const float* cur = (k0 == 0) ? src : dst;
 
@@ -347,6 +353,13 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
       }
       __syncthreads();
     }
+    if constexpr (SPLIT) {
+      // hand the row map and L11^-1 to the trailing-update launch
+      if (PIVOT)
+        for (int i = k0 + tid; i < n; i += T) a.perm[(int64_t)b * n + i] = pl[i];
+      for (int idx = tid; idx < NB * NB; idx += T) a.X[(int64_t)b * NB * NB + idx] = P[sw(idx / NB, idx % NB)];
+      return;
+    }
 
     // ---- trailing update, 64 columns at a time
     for (int c0 = k1; c0 < n; c0 += 64) {
@@ -424,6 +437,86 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
         L[idx] = (j < i) ? dst[(int64_t)pl[i] * n + j] : (j == i ? 1.f : 0.f);
       }
     }
+  }
+}
+
+// Trailing update of panel a.k0 for SPLIT launches: one 256-thread workgroup per 64-column
+// chunk of the trailing columns of one matrix, the same arithmetic as k_lu's fused update:
+// -U12 = -(L11^-1 A12[:, chunk]) on 16x16x4 MFMA, then A22[:, chunk] += L21 (-U12) on
+// 32x32x2 MFMA in 32-row tiles, L21 staged per tile through LDS.  Rows are addressed through
+// the row map in a.perm (LU) or directly (chart).
+constexpr int kLuTrailThreads = 256;
+
+template <bool PIVOT, int NB>
+__global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail(LuArgs a, int nchunk) {
+  constexpr int NW = kLuTrailThreads / 64, NB4 = NB / 4;
+  __shared__ float Xs[NB][NB + 1];
+  __shared__ float U[NB][64];
+  __shared__ float Ls[NW][32][NB + 1];
+  __shared__ int pls[RNR_MAX_N];
+  const int n = a.n, k0 = a.k0, k1 = k0 + NB;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int l32 = lane & 31, h = lane >> 5, l16 = lane & 15, q4 = lane >> 4;
+  const int64_t pid = blockIdx.x;
+  const int64_t b = pid / nchunk;
+  const int c0 = k1 + 64 * (int)(pid - b * nchunk);
+  const float* cur = ((k0 == 0) ? a.src + b * a.ss : a.dst + b * a.sd);
+  float* dst = a.dst + b * a.sd;
+  for (int i = k0 + tid; i < n; i += kLuTrailThreads) pls[i] = PIVOT ? a.perm[b * n + i] : i;
+  for (int idx = tid; idx < NB * NB; idx += kLuTrailThreads) Xs[idx / NB][idx % NB] = a.X[b * NB * NB + idx];
+  __syncthreads();
+
+  // -U12 chunk: (NB/16) x 4 blocks of 16x16
+  {
+    constexpr int NJOB = (NB / 16) * 4;
+    for (int job = wid; job < NJOB; job += NW) {
+      const int bi = job >> 2, bj = job & 3;
+      const int col = c0 + bj * 16 + l16;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < NB4; ++t) {
+        const int k = 4 * t + q4;
+        const float bv = (col < n) ? cur[pls[k0 + k] * n + col] : 0.f;
+        acc = mfma16(Xs[bi * 16 + l16][k], bv, acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) U[bi * 16 + 4 * q4 + r][bj * 16 + l16] = -acc[r];
+    }
+  }
+  __syncthreads();
+
+  const int ntr = (n - k1 + 31) >> 5;
+  for (int tr = wid; tr < ntr; tr += NW) {
+    const int r0 = k1 + tr * 32;
+    // L21 rows r0 .. r0 + 31 (columns k0 .. k1) into this wave's tile
+    for (int idx = lane; idx < 32 * NB; idx += 64) {
+      const int rr = idx / NB, k = idx - rr * NB, rw = r0 + rr;
+      Ls[wid][rr][k] = (rw < n) ? dst[pls[rw] * n + k0 + k] : 0.f;
+    }
+    wave_lds_order();
+    f32x16 c[2];
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rw = r0 + acc_row(r, lane), col = c0 + nj * 32 + l32;
+        c[nj][r] = (rw < n && col < n) ? cur[pls[rw] * n + col] : 0.f;
+      }
+#pragma unroll
+    for (int kk = 0; kk < NB; kk += 2) {
+      const int k = kk + h;
+      const float av = Ls[wid][l32][k];
+      c[0] = mfma(av, U[k][l32], c[0]);
+      c[1] = mfma(av, U[k][32 + l32], c[1]);
+    }
+    wave_lds_order();  // the next tile's L21 stores stay behind these reads
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rw = r0 + acc_row(r, lane), col = c0 + nj * 32 + l32;
+        if (rw < n && col < n) dst[pls[rw] * n + col] = c[nj][r];
+      }
   }
 }
 

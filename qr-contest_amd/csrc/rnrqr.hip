@@ -76,7 +76,7 @@ size_t carve(int64_t batch, int64_t n, unsigned need, char* base, Ws* ws) {
 }
 
 constexpr unsigned kQrNeed = kNeedW | kNeedL | kNeedG | kNeedQb | kNeedDinv | kNeedS | kNeedPerm | kNeedInfo;
-constexpr unsigned kLuNeed = kNeedW;
+constexpr unsigned kLuNeed = kNeedW | kNeedDinv;
 constexpr unsigned kCholqrNeed = kNeedG | kNeedQb | kNeedDinv | kNeedInfo;
 constexpr unsigned kFrameNeed = kNeedW | kNeedL | kNeedG | kNeedQb | kNeedDinv | kNeedPerm | kNeedInfo;
 
@@ -109,13 +109,40 @@ int launch_lu_nb(const LuArgs& a, int64_t batch, hipStream_t st) {
   return hip_status();
 }
 
+// Batches too small to occupy the GPU with one workgroup per matrix (fewer matrices than
+// half the CUs) at n > 512: each panel is its own launch, and its trailing update is spread
+// over one workgroup per 64-column chunk (k_lu_trail).
+bool lu_split(int64_t batch, int n) { return n > 512 && batch < 128; }
+
+template <bool PIVOT, int NB, int RPT>
+int launch_lu_split(LuArgs a, int64_t batch, hipStream_t st) {
+  const size_t lds = lu_lds_bytes(a.n, NB);
+  if (lds > kLdsMax) return RNR_ERR_UNSUPPORTED_N;
+  if (int e = set_lds(k_lu<PIVOT, NB, RPT, true>, lds)) return e;
+  for (int k0 = 0; k0 < a.n; k0 += NB) {
+    a.k0 = k0;
+    k_lu<PIVOT, NB, RPT, true><<<dim3((unsigned)batch), dim3(kLuThreads), lds, st>>>(a);
+    const int k1 = k0 + NB;
+    if (k1 >= a.n) break;
+    const int nchunk = (a.n - k1 + 63) / 64;
+    k_lu_trail<PIVOT, NB><<<dim3((unsigned)(batch * nchunk)), dim3(kLuTrailThreads), 0, st>>>(a, nchunk);
+  }
+  return hip_status();
+}
+
+// xbuf: [batch][64][64] floats of scratch for the split form (L11^-1 between launches).
 int launch_lu(bool pivot, const float* src, int64_t ss, float* dst, int64_t sd, int64_t batch,
-              int n, int* perm, float* L, float* s, float* tau, hipStream_t st) {
+              int n, int* perm, float* L, float* s, float* tau, float* xbuf, hipStream_t st) {
   LuArgs a;
   a.src = src; a.ss = ss; a.dst = dst; a.sd = sd; a.n = n;
   a.vec4 = (n % 4 == 0) && (ss % 4 == 0) && (sd % 4 == 0) && aligned(src, 16) && aligned(dst, 16);
   a.perm = perm; a.L = L; a.sl = (int64_t)n * n; a.s = s; a.tau = tau;
+  a.k0 = 0; a.X = xbuf;
   const int nb = lu_panel_nb(n);
+  if (lu_split(batch, n) && xbuf) {
+    if (pivot) return nb == 32 ? launch_lu_split<true, 32, 2>(a, batch, st) : launch_lu_split<true, 16, 4>(a, batch, st);
+    return nb == 32 ? launch_lu_split<false, 32, 2>(a, batch, st) : launch_lu_split<false, 16, 4>(a, batch, st);
+  }
   // rows per thread: n <= kLuThreads * RPT
   if (pivot) {
     if (nb == 64) return launch_lu_nb<true, 64, 1>(a, batch, st);
@@ -251,7 +278,8 @@ int frame(const float* A, int64_t sa, const Ws& w, float* Q, float* Qcopy, int* 
           int n, hipStream_t st, Marks& mk) {
   const int64_t nn = (int64_t)n * n;
   if (int e = mk.mark(st)) return e;
-  if (int e = launch_lu(true, A, sa, w.W, nn, batch, n, w.perm, nullptr, nullptr, nullptr, st)) return e;
+  if (int e = launch_lu(true, A, sa, w.W, nn, batch, n, w.perm, nullptr, nullptr, nullptr, w.Dinv, st))
+    return e;
   // W (the solve's off-diagonal operand) lives in Qb for the first pass and in the then
   // dead LU buffer for the second
   if (int e = cholqr_pass(w.W, nn, w.perm, w.G, w.Dinv, w.Qb, info, false, w.L, nullptr, nullptr, batch, n,
@@ -286,7 +314,7 @@ int qr_path(const float* A, int64_t batch, int64_t n, int64_t batch_stride, floa
   int* inf = info ? info : w.info;
   if (int e = frame(A, batch_stride, w, w.Qb, H, inf, batch, ni, st, mk)) return e;
   if (int e = mk.mark(st)) return e;
-  if (int e = launch_lu(false, H, nn, H, nn, batch, ni, nullptr, nullptr, w.s, tau, st)) return e;
+  if (int e = launch_lu(false, H, nn, H, nn, batch, ni, nullptr, nullptr, w.s, tau, w.Dinv, st)) return e;
   if (int e = mk.mark(st)) return e;
   if (int e = launch_tn(true, w.Qb, nn, A, batch_stride, H, nn, w.s, nullptr, batch, ni, false, st))
     return e;
@@ -353,7 +381,7 @@ int rnr_lu_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride, f
   if (int e = check_ws(ws, ws_bytes, need)) return e;
   Ws w;
   carve(batch, n, kLuNeed, static_cast<char*>(ws), &w);
-  return launch_lu(true, A, batch_stride, w.W, n * n, batch, (int)n, perm, L, nullptr, nullptr,
+  return launch_lu(true, A, batch_stride, w.W, n * n, batch, (int)n, perm, L, nullptr, nullptr, w.Dinv,
                    reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -408,7 +436,8 @@ int rnr_chart_f32(float* Y, int64_t batch, int64_t n, float* s, float* tau, rnr_
   if (!Y || !s || !tau) return RNR_ERR_INVALID_ARG;
   if (!aligned(Y, 4) || !aligned(s, 4) || !aligned(tau, 4)) return RNR_ERR_MISALIGNED;
   const int64_t nn = n * n;
-  return launch_lu(false, Y, nn, Y, nn, batch, (int)n, nullptr, nullptr, s, tau,
+  // no workspace here: the fused one-workgroup-per-matrix form at every batch size
+  return launch_lu(false, Y, nn, Y, nn, batch, (int)n, nullptr, nullptr, s, tau, nullptr,
                    reinterpret_cast<hipStream_t>(stream));
 }
 

@@ -209,10 +209,28 @@ def test_repeat_runs_are_bitwise_identical(rnr, wl):
     assert torch.equal(H1, H2) and torch.equal(t1, t2)
 
 
+@pytest.mark.parametrize("n", [640, 1100])
+def test_split_panels_equal_the_fused_kernels(rnr, wl, n):
+    """Small batches at n > 512 factor each LU / chart panel in its own launch and spread the
+    trailing update over workgroups; the arithmetic is the fused kernel's, operation for
+    operation, so the results must match a batch large enough for the fused form bit for bit."""
+    print(f"[case] split vs fused n={n}", flush=True)
+    A2 = wl.make_batch(4, batch=2, n=n, seed=7).to(DEV)
+    big = A2.repeat(65, 1, 1)  # 130 matrices: one workgroup per matrix
+    H2, t2 = rnr.custom_kernel(A2)
+    Hb, tb = rnr.custom_kernel(big)
+    p2, L2 = rnr.lu(A2)
+    pb, Lb = rnr.lu(big)
+    torch.cuda.synchronize()
+    assert torch.equal(H2, Hb[:2]) and torch.equal(t2, tb[:2])
+    assert torch.equal(H2, Hb[128:130]) and torch.equal(p2, pb[128:130]) and torch.equal(L2, Lb[:2])
+    _gates(A2.cpu(), H2.cpu(), t2.cpu(), f"split n={n}")
+
+
 # ----------------------------------------------------------------------------- stages
 
 
-@pytest.mark.parametrize("n", [7, 64, 130, 512])
+@pytest.mark.parametrize("n", [7, 64, 130, 512, 700])
 def test_stage_lu_matches_getrf(rnr, wl, n):
     g = torch.Generator().manual_seed(n)
     A = torch.randn(3, n, n, generator=g)
