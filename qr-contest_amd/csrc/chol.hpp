@@ -309,4 +309,153 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
   }
 }
 
+// ---- split form: batches too small to fill the GPU with one workgroup per matrix ----------
+// The same arithmetic as k_chol, operation for operation, in four kinds of launches per
+// matrix batch: the jitter once, then per 64-column block the diagonal factor and inverse
+// (one wave per matrix), the block row (one wave per 32 columns) and the trailing update (one
+// wave per upper 64x64 tile).  The diagonal tile goes through G instead of staying in LDS.
+constexpr int kCholSplitThreads = 256;
+
+struct CholSplitArgs {
+  float* G;
+  int64_t sg;
+  float* Dinv;
+  int* info;
+  int n, k0, keep_info, njob;
+};
+
+__global__ __launch_bounds__(kCholThreads) void k_chol_jitter(CholSplitArgs a) {
+  __shared__ float red[kCholThreads / 64];
+  constexpr int NW = kCholThreads / 64;
+  const int n = a.n, b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  float* G = a.G + b * a.sg;
+  float part = 0.f;
+  for (int i = tid; i < n; i += kCholThreads) part += G[(int64_t)i * n + i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+  if (lane == 0) red[wid] = part;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) tot += red[w];
+  const float mu = 1e-7f * (tot / (float)n);
+  for (int i = tid; i < n; i += kCholThreads) G[(int64_t)i * n + i] += mu;
+  if (tid == 0 && (!a.keep_info || a.info[b] == 0)) a.info[b] = 0;
+}
+
+__global__ __launch_bounds__(64) void k_chol_diag(CholSplitArgs a) {
+  __shared__ float D[64 * 65];
+  __shared__ float XT[64 * 68];  // RT while factoring, then XT
+  __shared__ float RI[64];
+  __shared__ float SB[64];
+  const int n = a.n, k0 = a.k0, b = blockIdx.x, lane = threadIdx.x;
+  const int kb = min(kCholNb, n - k0);
+  float* G = a.G + b * a.sg;
+  float* Dv = a.Dinv + (int64_t)b * n * 64;
+  for (int idx = lane; idx < 64 * 64; idx += 64) {
+    const int i = idx >> 6, c = idx & 63;
+    D[i * 65 + c] = (i < kb && c < kb) ? G[(k0 + i) * n + k0 + c] : (i == c ? 1.f : 0.f);
+  }
+  wave_lds_order();
+  const int fail = chol_diag_wave(D, XT, RI, SB, lane);
+  if (lane == 0 && fail != INT_MAX && fail < kb && a.info[b] == 0) a.info[b] = k0 + fail + 1;
+  wave_lds_order();
+  chol_inverse_wave(XT, RI, XT, lane);
+  wave_lds_order();
+  for (int idx = lane; idx < kb * 64; idx += 64) {
+    const int i = idx >> 6, c = idx & 63;
+    if (c < kb && c >= i) G[(k0 + i) * n + k0 + c] = D[i * 65 + c];
+    Dv[(k0 + i) * 64 + c] = (c < kb) ? XT[c * 65 + i] : 0.f;
+  }
+}
+
+// R_k,> = Dinv_kk^T G_k,>: wave w of workgroup g takes the 32 columns starting at
+// k1 + 32 (4 g + w).
+__global__ __launch_bounds__(kCholSplitThreads) void k_chol_row(CholSplitArgs a) {
+  __shared__ float XT[64 * 65];
+  const int n = a.n, k0 = a.k0, k1 = k0 + kCholNb, w = n - k1;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, l32 = lane & 31, h = lane >> 5;
+  const int64_t pid = blockIdx.x;
+  const int64_t b = pid / a.njob;
+  const int job = 4 * (int)(pid - b * a.njob) + wid;
+  float* G = a.G + b * a.sg;
+  const float* Dv = a.Dinv + b * n * 64;
+  for (int idx = tid; idx < 64 * 64; idx += kCholSplitThreads) {
+    const int i = idx >> 6, c = idx & 63;  // XT[c][i] = Dinv_kk[i][c]
+    XT[c * 65 + i] = Dv[(k0 + i) * 64 + c];
+  }
+  __syncthreads();
+  if (32 * job >= w) return;
+  const int colr = job * 32 + l32, col = k1 + colr;
+  const int base = (k0 + h) * n + col;
+  float bv[32];
+#pragma unroll
+  for (int t = 0; t < 32; ++t) bv[t] = (col < n) ? G[base + 2 * t * n] : 0.f;
+  f32x16 acc0 = zero16(), acc1 = zero16();
+#pragma unroll
+  for (int t = 0; t < 32; ++t) {
+    const int k = 2 * t + h;
+    acc0 = mfma(XT[l32 * 65 + k], bv[t], acc0);
+    acc1 = mfma(XT[(32 + l32) * 65 + k], bv[t], acc1);
+  }
+  if (col < n) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i0 = acc_row(r, lane), i1 = 32 + acc_row(r, lane);
+      G[(k0 + i0) * n + col] = acc0[r];
+      G[(k0 + i1) * n + col] = acc1[r];
+    }
+  }
+}
+
+// G_>,> -= R_k,>^T R_k,>: wave w of workgroup g takes upper tile pair 4 g + w.
+__global__ __launch_bounds__(kCholSplitThreads) void k_chol_trail(CholSplitArgs a) {
+  const int n = a.n, k0 = a.k0, k1 = k0 + kCholNb, w = n - k1;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, l32 = lane & 31, h = lane >> 5;
+  const int nt = (w + 63) >> 6, npairs = nt * (nt + 1) / 2;
+  const int64_t pid = blockIdx.x;
+  const int64_t b = pid / a.njob;
+  const int pr = 4 * (int)(pid - b * a.njob) + wid;
+  if (pr >= npairs) return;
+  float* G = a.G + b * a.sg;
+  int I, J;
+  upper_tile(pr, nt, I, J);
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = k1 + I * 64 + mi * 32 + acc_row(r, lane);
+        const int col = k1 + J * 64 + nj * 32 + l32;
+        acc[mi][nj][r] = (row < n && col < n) ? G[row * n + col] : 0.f;
+      }
+#pragma unroll 4
+  for (int kk = 0; kk < kCholNb; kk += 2) {
+    const int k = kk + h;
+    float av[2], bv[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int ci = I * 64 + q * 32 + l32, cj = J * 64 + q * 32 + l32;
+      av[q] = (ci < w) ? -G[(k0 + k) * n + k1 + ci] : 0.f;
+      bv[q] = (cj < w) ? G[(k0 + k) * n + k1 + cj] : 0.f;
+    }
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = mfma(av[mi], bv[nj], acc[mi][nj]);
+  }
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = k1 + I * 64 + mi * 32 + acc_row(r, lane);
+        const int col = k1 + J * 64 + nj * 32 + l32;
+        if (row < n && col < n) G[row * n + col] = acc[mi][nj][r];
+      }
+}
+
 }  // namespace rnr

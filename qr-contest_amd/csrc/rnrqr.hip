@@ -110,8 +110,9 @@ int launch_lu_nb(const LuArgs& a, int64_t batch, hipStream_t st) {
 }
 
 // Batches too small to occupy the GPU with one workgroup per matrix (fewer matrices than
-// half the CUs) at n > 512: each panel is its own launch, and its trailing update is spread
-// over one workgroup per 64-column chunk (k_lu_trail).
+// half the CUs) at n > 512: each LU / chart panel is its own launch, and its trailing update is
+// spread over one workgroup per 64-column chunk (k_lu_trail); the Cholesky likewise runs per
+// block (k_chol_diag / k_chol_row / k_chol_trail).
 bool lu_split(int64_t batch, int n) { return n > 512 && batch < 128; }
 
 template <bool PIVOT, int NB, int RPT>
@@ -203,10 +204,28 @@ int launch_chol(float* G, int64_t sg, float* Dinv, float* Wm, int* info, int64_t
   CholArgs a;
   a.G = G; a.sg = sg; a.Dinv = Dinv; a.info = info; a.n = n;
   a.keep_info = keep_info ? 1 : 0;
-  a.strip_lds = chol_lds_bytes(n, true) <= kLdsMax ? 1 : 0;
-  const size_t lds = chol_lds_bytes(n, a.strip_lds != 0);
-  if (int e = set_lds(k_chol, lds)) return e;
-  k_chol<<<dim3((unsigned)batch), dim3(kCholThreads), lds, st>>>(a);
+  if (lu_split(batch, n)) {
+    // small batch: per 64-column block a diagonal launch (one wave per matrix), then the
+    // block row and the trailing tiles spread over one wave per 32 columns / per tile
+    CholSplitArgs c{G, sg, Dinv, info, n, 0, a.keep_info, 0};
+    k_chol_jitter<<<dim3((unsigned)batch), dim3(kCholThreads), 0, st>>>(c);
+    for (int k0 = 0; k0 < n; k0 += kCholNb) {
+      c.k0 = k0;
+      k_chol_diag<<<dim3((unsigned)batch), dim3(64), 0, st>>>(c);
+      const int w = n - k0 - kCholNb;
+      if (w <= 0) break;
+      c.njob = (w + 127) / 128;
+      k_chol_row<<<dim3((unsigned)(batch * c.njob)), dim3(kCholSplitThreads), 0, st>>>(c);
+      const int nt = (w + 63) / 64;
+      c.njob = (nt * (nt + 1) / 2 + 3) / 4;
+      k_chol_trail<<<dim3((unsigned)(batch * c.njob)), dim3(kCholSplitThreads), 0, st>>>(c);
+    }
+  } else {
+    a.strip_lds = chol_lds_bytes(n, true) <= kLdsMax ? 1 : 0;
+    const size_t lds = chol_lds_bytes(n, a.strip_lds != 0);
+    if (int e = set_lds(k_chol, lds)) return e;
+    k_chol<<<dim3((unsigned)batch), dim3(kCholThreads), lds, st>>>(a);
+  }
   if (int e = hip_status()) return e;
   return launch_wblocks(G, sg, Dinv, Wm, batch, n, st);
 }
