@@ -440,15 +440,18 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
   }
 }
 
-// Trailing update of panel a.k0 for SPLIT launches: one 256-thread workgroup per 64-column
-// chunk of the trailing columns of one matrix, the same arithmetic as k_lu's fused update:
+// Trailing update of panel a.k0 for SPLIT launches: one 256-thread workgroup per (64-column
+// chunk, 256-row group) of the trailing matrix of one matrix, the same arithmetic as k_lu's
+// fused update (each workgroup forms its chunk's -U12 itself):
 // -U12 = -(L11^-1 A12[:, chunk]) on 16x16x4 MFMA, then A22[:, chunk] += L21 (-U12) on
 // 32x32x2 MFMA in 32-row tiles, L21 staged per tile through LDS.  Rows are addressed through
 // the row map in a.perm (LU) or directly (chart).
 constexpr int kLuTrailThreads = 256;
 
+constexpr int kLuTrailRows = 256;  // rows per workgroup (eight 32-row tiles)
+
 template <bool PIVOT, int NB>
-__global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail(LuArgs a, int nchunk) {
+__global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail(LuArgs a, int nchunk, int nrg) {
   constexpr int NW = kLuTrailThreads / 64, NB4 = NB / 4;
   __shared__ float Xs[NB][NB + 1];
   __shared__ float U[NB][64];
@@ -458,8 +461,9 @@ __global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail(LuArgs a, int nchu
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5, l16 = lane & 15, q4 = lane >> 4;
   const int64_t pid = blockIdx.x;
-  const int64_t b = pid / nchunk;
-  const int c0 = k1 + 64 * (int)(pid - b * nchunk);
+  const int64_t b = pid / ((int64_t)nchunk * nrg);
+  const int rem = (int)(pid - b * nchunk * nrg), rg = rem / nchunk;
+  const int c0 = k1 + 64 * (rem - rg * nchunk);
   const float* cur = ((k0 == 0) ? a.src + b * a.ss : a.dst + b * a.sd);
   float* dst = a.dst + b * a.sd;
   for (int i = k0 + tid; i < n; i += kLuTrailThreads) pls[i] = PIVOT ? a.perm[b * n + i] : i;
@@ -485,8 +489,8 @@ __global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail(LuArgs a, int nchu
   }
   __syncthreads();
 
-  const int ntr = (n - k1 + 31) >> 5;
-  for (int tr = wid; tr < ntr; tr += NW) {
+  const int ntr = min((n - k1 + 31) >> 5, (rg + 1) * (kLuTrailRows / 32));
+  for (int tr = rg * (kLuTrailRows / 32) + wid; tr < ntr; tr += NW) {
     const int r0 = k1 + tr * 32;
     // L21 rows r0 .. r0 + 31 (columns k0 .. k1) into this wave's tile
     for (int idx = lane; idx < 32 * NB; idx += 64) {

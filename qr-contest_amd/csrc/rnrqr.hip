@@ -125,8 +125,8 @@ int launch_lu_split(LuArgs a, int64_t batch, hipStream_t st) {
     k_lu<PIVOT, NB, RPT, true><<<dim3((unsigned)batch), dim3(kLuThreads), lds, st>>>(a);
     const int k1 = k0 + NB;
     if (k1 >= a.n) break;
-    const int nchunk = (a.n - k1 + 63) / 64;
-    k_lu_trail<PIVOT, NB><<<dim3((unsigned)(batch * nchunk)), dim3(kLuTrailThreads), 0, st>>>(a, nchunk);
+    const int nchunk = (a.n - k1 + 63) / 64, nrg = (a.n - k1 + kLuTrailRows - 1) / kLuTrailRows;
+    k_lu_trail<PIVOT, NB><<<dim3((unsigned)(batch * nchunk * nrg)), dim3(kLuTrailThreads), 0, st>>>(a, nchunk, nrg);
   }
   return hip_status();
 }
