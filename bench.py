@@ -43,23 +43,32 @@ def _events_ms(fn, reps: int, stream) -> float:
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_headline_256x512.md")
 # bench kernel label -> the kernel symbol in the rocprofv3 counter summary
-PROFILE_SYMBOL = {"k_trsm": "rnr::k_trsm<true>", "k_chol": "rnr::k_chol",
-                  "k_lu<true> (LU)": "rnr::k_lu<true, 64, 1>", "k_lu<false> (chart)": "rnr::k_lu<false, 64, 1>",
-                  "k_tn_upper": "rnr::k_tn_upper<128, false, false, true>"}
+# rocprofv3 symbols of each reported kernel and their launches per step
+PROFILE_SYMBOL = {"k_trsm": [("rnr::k_trsm<true>", 2)], "k_chol": [("rnr::k_chol", 2)],
+                  "k_lu<true> (LU)": [("rnr::k_lu<true, 64, 1, false>", 1)],
+                  "k_lu<false> (chart)": [("rnr::k_lu<false, 64, 1, false>", 1)],
+                  "k_tn_upper": [("rnr::k_tn_upper<128, false, false, true>", 2),
+                                 ("rnr::k_tn_upper<128, true, true, true>", 1)]}
 
 
 def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH/WRITE summary
-    (headline workload only), or None."""
-    sym = PROFILE_SYMBOL.get(kernel)
+    """HBM bytes per launch of `kernel` (mean over its launches in one step) from the committed
+    rocprofv3 FETCH/WRITE summary (headline workload only), or None."""
+    syms = PROFILE_SYMBOL.get(kernel)
+    if not syms:
+        return None
+    per = {}
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
-                if line.startswith("traffic ") and line[len("traffic "):].rsplit(" ", 1)[0] == sym:
-                    return int(line.rsplit(" ", 1)[1])
+                if line.startswith("traffic "):
+                    name, val = line[len("traffic "):].rsplit(" ", 1)
+                    per[name] = int(val)
     except OSError:
-        pass
-    return None
+        return None
+    if not all(s in per for s, _ in syms):
+        return None
+    return int(sum(per[s] * c for s, c in syms) / sum(c for _, c in syms))
 
 
 def _cpu_name() -> str:
