@@ -126,14 +126,19 @@ int rnr_generate_f32(int config, int64_t batch, int64_t n, uint64_t seed, float*
 
 /* ---- consumers of the path's output (README.md:122-128) ------------------------------
  * Q = householder_product(H, tau) (torch.linalg.householder_product), batch x n x n, all
- * contiguous. */
-int rnr_orgqr_f32(const float* H, const float* tau, int64_t batch, int64_t n, float* Q,
-                  rnr_stream_t stream);
+ * contiguous.  The workspace holds every panel's T (batch * ceil(n/32) * 4 KiB), 256-byte
+ * aligned. */
+int rnr_orgqr_f32_workspace(int64_t batch, int64_t n, size_t* bytes);
+int rnr_orgqr_f32(const float* H, const float* tau, int64_t batch, int64_t n, float* Q, void* workspace,
+                  size_t workspace_bytes, rnr_stream_t stream);
 
 /* C <- Q C (transpose == 0) or Q^T C (transpose != 0) in place (torch.ormqr, left side):
- * C is batch x n x ncol with row stride ldc >= ncol and batch stride >= n * ldc. */
+ * C is batch x n x ncol with row stride ldc >= ncol and batch stride >= n * ldc.  Same
+ * workspace as rnr_orgqr_f32. */
+int rnr_ormqr_f32_workspace(int64_t batch, int64_t n, size_t* bytes);
 int rnr_ormqr_f32(const float* H, const float* tau, int64_t batch, int64_t n, float* C, int64_t ncol,
-                  int64_t ldc, int64_t batch_stride_c, int transpose, rnr_stream_t stream);
+                  int64_t ldc, int64_t batch_stride_c, int transpose, void* workspace, size_t workspace_bytes,
+                  rnr_stream_t stream);
 
 /* ---- benchmark comparator (NOT on the reflector-free path) --------------------------------
  * Householder blocked-WY QR in torch.geqrf layout, in place on H (A in, H out), float32: the

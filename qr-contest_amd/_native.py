@@ -50,8 +50,10 @@ SIGNATURES = {
     "rnr_generate_f32": (_int, [_int, _i64, _i64, _u64, _vp, _vp, _sz, _vp]),
     "rnr_hh_geqrf_workspace": (_int, [_i64, _i64, _szp]),
     "rnr_hh_geqrf_f32": (_int, [_vp, _i64, _i64, _vp, _vp, _sz, _vp]),
-    "rnr_orgqr_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
-    "rnr_ormqr_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _int, _vp]),
+    "rnr_orgqr_f32_workspace": (_int, [_i64, _i64, _szp]),
+    "rnr_orgqr_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "rnr_ormqr_f32_workspace": (_int, [_i64, _i64, _szp]),
+    "rnr_ormqr_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _int, _vp, _sz, _vp]),
     "rnr_check_f64_workspace": (_int, [_i64, _i64, _szp]),
     "rnr_check_f64": (_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
 }
@@ -103,9 +105,10 @@ def check(fn: str, status: int) -> None:
 
 
 def workspace_bytes(kind: str, batch: int, n: int) -> int:
-    """Workspace size for one of "qr", "lu", "cholqr", "frame", "check", "hh_geqrf"."""
+    """Workspace size for one of "qr", "lu", "cholqr", "frame", "check", "hh_geqrf", "orgqr", "ormqr"."""
     out = ctypes.c_size_t(0)
-    name = {"check": "rnr_check_f64_workspace", "hh_geqrf": "rnr_hh_geqrf_workspace"}.get(
+    name = {"check": "rnr_check_f64_workspace", "hh_geqrf": "rnr_hh_geqrf_workspace",
+            "orgqr": "rnr_orgqr_f32_workspace", "ormqr": "rnr_ormqr_f32_workspace"}.get(
         kind, f"rnr_{kind}_f32_workspace")
     check(name, getattr(lib(), name)(int(batch), int(n), ctypes.byref(out)))
     return int(out.value)

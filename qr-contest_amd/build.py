@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 SOURCES = ["rnrqr.hip", "small.hip", "check.hip", "orgqr.hip", "gen.hip", "hhqr.hip"]
-HEADERS = ["common.hpp", "gemm_tn.hpp", "lu.hpp", "chol.hpp", "trsm.hpp", "small.hpp", "applyq.hpp"]
+HEADERS = ["common.hpp", "gemm_tn.hpp", "lu.hpp", "chol.hpp", "trsm.hpp", "small.hpp", "applyq.hpp", "wy.hpp"]
 OUT = os.path.join(HERE, "librnrqr.so")
 ARCH = os.environ.get("RNR_OFFLOAD_ARCH", "gfx950")
 

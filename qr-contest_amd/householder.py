@@ -6,7 +6,8 @@ reference: ``Q = torch.linalg.householder_product(H, tau)``, ``R = triu(H)``).
   ``left=True``).
 
 Both take ``(..., n, n)`` H, ``(..., n)`` tau and work in float32 on the tensors' GPU, on the
-current stream; the result comes back in H's dtype.
+current stream, with blocked-WY updates on MFMA (32-reflector panels); the result comes back in
+H's dtype.
 """
 from __future__ import annotations
 
@@ -34,9 +35,11 @@ def householder_product(H: torch.Tensor, tau: torch.Tensor) -> torch.Tensor:
     batch = Hf.shape[0]
     Q = torch.empty_like(Hf)
     if batch:
+        need = _native.workspace_bytes("orgqr", batch, n)
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=Hf.device)
         with torch.cuda.device(Hf.device):
-            st = _native.lib().rnr_orgqr_f32(Hf.data_ptr(), tf.data_ptr(), batch, n, Q.data_ptr(),
-                                             torch.cuda.current_stream(Hf.device).cuda_stream)
+            st = _native.lib().rnr_orgqr_f32(Hf.data_ptr(), tf.data_ptr(), batch, n, Q.data_ptr(), ws.data_ptr(),
+                                             need, torch.cuda.current_stream(Hf.device).cuda_stream)
         _native.check("rnr_orgqr_f32", st)
     return Q.reshape(H.shape).to(H.dtype)
 
@@ -52,9 +55,11 @@ def ormqr(H: torch.Tensor, tau: torch.Tensor, C: torch.Tensor, transpose: bool =
     Y = C.to(torch.float32).reshape(-1, n, k).clone(memory_format=torch.contiguous_format)
     batch = Y.shape[0]
     if batch and k:
+        need = _native.workspace_bytes("ormqr", batch, n)
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=Y.device)
         with torch.cuda.device(Y.device):
             st = _native.lib().rnr_ormqr_f32(Hf.data_ptr(), tf.data_ptr(), batch, n, Y.data_ptr(), k, k, n * k,
-                                             1 if transpose else 0,
+                                             1 if transpose else 0, ws.data_ptr(), need,
                                              torch.cuda.current_stream(Y.device).cuda_stream)
         _native.check("rnr_ormqr_f32", st)
     return Y.reshape(C.shape).to(C.dtype)

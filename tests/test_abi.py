@@ -130,17 +130,23 @@ def test_argument_validation_before_any_launch(native, lib):
     assert hq(fake, 2, 16, fake, fake + 8, hw.value, None) == native.RNR_ERR_MISALIGNED
     assert hq(None, 0, 16, None, None, 0, None) == native.RNR_OK
     # the Q consumers
+    qw = native.workspace_bytes("orgqr", 2, 100)
+    assert qw >= 2 * 4 * 32 * 32 * 4 and native.workspace_bytes("ormqr", 2, 100) == qw
     o = lib.rnr_orgqr_f32
-    assert o(None, fake, 2, 16, fake, None) == native.RNR_ERR_INVALID_ARG
-    assert o(fake, fake, 2, 0, fake, None) == native.RNR_ERR_UNSUPPORTED_N
-    assert o(fake, fake, 2, 4096, fake, None) == native.RNR_ERR_UNSUPPORTED_N
-    assert o(None, None, 0, 16, None, None) == native.RNR_OK
+    assert o(None, fake, 2, 16, fake, fake, qw, None) == native.RNR_ERR_INVALID_ARG
+    assert o(fake, fake, 2, 0, fake, fake, qw, None) == native.RNR_ERR_UNSUPPORTED_N
+    assert o(fake, fake, 2, 4096, fake, fake, qw, None) == native.RNR_ERR_UNSUPPORTED_N
+    assert o(fake, fake, 2, 100, fake, None, qw, None) == native.RNR_ERR_WORKSPACE
+    assert o(fake, fake, 2, 100, fake, fake, qw - 1, None) == native.RNR_ERR_WORKSPACE
+    assert o(fake, fake, 2, 100, fake, fake + 8, qw, None) == native.RNR_ERR_MISALIGNED
+    assert o(None, None, 0, 16, None, None, 0, None) == native.RNR_OK
     m = lib.rnr_ormqr_f32
-    assert m(fake, fake, 2, 16, None, 5, 5, 80, 0, None) == native.RNR_ERR_INVALID_ARG
-    assert m(fake, fake, 2, 16, fake, 5, 4, 80, 0, None) == native.RNR_ERR_INVALID_ARG   # ldc < ncol
-    assert m(fake, fake, 2, 16, fake, 5, 5, 79, 1, None) == native.RNR_ERR_INVALID_ARG   # stride < n ldc
-    assert m(fake, fake, 2, 16, fake, -1, 5, 80, 1, None) == native.RNR_ERR_INVALID_ARG
-    assert m(None, None, 2, 16, None, 0, 0, 0, 1, None) == native.RNR_OK
+    assert m(fake, fake, 2, 16, None, 5, 5, 80, 0, fake, qw, None) == native.RNR_ERR_INVALID_ARG
+    assert m(fake, fake, 2, 16, fake, 5, 4, 80, 0, fake, qw, None) == native.RNR_ERR_INVALID_ARG   # ldc < ncol
+    assert m(fake, fake, 2, 16, fake, 5, 5, 79, 1, fake, qw, None) == native.RNR_ERR_INVALID_ARG   # stride < n ldc
+    assert m(fake, fake, 2, 16, fake, -1, 5, 80, 1, fake, qw, None) == native.RNR_ERR_INVALID_ARG
+    assert m(fake, fake, 2, 100, fake, 5, 5, 500, 1, None, qw, None) == native.RNR_ERR_WORKSPACE
+    assert m(None, None, 2, 16, None, 0, 0, 0, 1, None, 0, None) == native.RNR_OK
 
 
 def test_python_layer_rejects_cpu_and_non_square(pkg):
