@@ -11,7 +11,7 @@
 //
 // Tile BM x BM per 256-thread workgroup (2 x 2 waves, each BM/2 x BM/2 from 32x32 MFMA
 // blocks); the K dimension (rows of X and Y) is staged through double-buffered LDS in
-// chunks of 32 rows, so every operand element is read from HBM/L2 once per tile.
+// chunks of BK rows, so every operand element is read from HBM/L2 once per tile.
 #pragma once
 #include "common.hpp"
 
@@ -34,9 +34,8 @@ struct TnArgs {
   int klo_from_j;
 };
 
-template <int BM, bool MASK_LOWER, bool ROW_SCALE, bool VEC4>
+template <int BM, bool MASK_LOWER, bool ROW_SCALE, bool VEC4, int BK = 32>
 __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
-  constexpr int BK = 32;
   constexpr int WM = BM / 2;
   constexpr int NB = WM / 32;
   constexpr int PER = BK * BM / 256;  // elements per thread per operand per chunk

@@ -175,6 +175,10 @@ int launch_tn(bool closure, const float* X, int64_t sx, const float* Y, int64_t 
   if (closure) {
     if (big) { if (vec4) RNR_TN(128, true, true, true); else RNR_TN(128, true, true, false); }
     else     { if (vec4) RNR_TN(64, true, true, true);  else RNR_TN(64, true, true, false); }
+  } else if (big && vec4) {
+    // the Grams: 16-row K chunks halve the LDS, so more workgroups per CU cover each tile's
+    // fixed load / store latency (the short K ranges of the Gram of L gain most)
+    k_tn_upper<128, false, false, true, 16><<<grid, block, 0, st>>>(a);
   } else {
     if (big) { if (vec4) RNR_TN(128, false, false, true); else RNR_TN(128, false, false, false); }
     else     { if (vec4) RNR_TN(64, false, false, true);  else RNR_TN(64, false, false, false); }
