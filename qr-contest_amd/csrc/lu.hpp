@@ -365,23 +365,33 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
     for (int c0 = k1; c0 < n; c0 += 64) {
       // -U12 = -(X A12[:, c0:c0+64]) as (NB/16) x 4 blocks of 16x16 spread over the waves
       {
-        constexpr int NBI = NB / 16, NJOB = NBI * 4;
-        for (int job = wid; job < NJOB; job += NW) {
-          const int bi = job >> 2, bj = job & 3;
+        // a wave's jobs load their A12 columns first, then multiply: one load latency per
+        // chunk instead of one per job
+        constexpr int NBI = NB / 16, NJOB = NBI * 4, JPW = (NJOB + NW - 1) / NW;
+        float bv[JPW][NB4];
+#pragma unroll
+        for (int u = 0; u < JPW; ++u) {
+          const int job = wid + u * NW, bj = job & 3;
           const int col = c0 + bj * 16 + l16;
-          float bv[NB4];
 #pragma unroll
           for (int t = 0; t < NB4; ++t) {
             const int k = 4 * t + q4;
             const int pr = PIVOT ? pl[k0 + k] : k0 + k;
-            bv[t] = (col < n) ? cur[(int64_t)pr * n + col] : 0.f;
+            bv[u][t] = (job < NJOB && col < n) ? cur[(int64_t)pr * n + col] : 0.f;
           }
-          const int i = bi * 16 + l16;
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
-          for (int t = 0; t < NB4; ++t) acc = mfma16(P[sw(i, 4 * t + q4)], bv[t], acc);
+        for (int u = 0; u < JPW; ++u) {
+          const int job = wid + u * NW;
+          if (job < NJOB) {
+            const int bi = job >> 2, bj = job & 3;
+            const int i = bi * 16 + l16;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) U[(bi * 16 + 4 * q4 + r) * 64 + bj * 16 + l16] = -acc[r];
+            for (int t = 0; t < NB4; ++t) acc = mfma16(P[sw(i, 4 * t + q4)], bv[u][t], acc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) U[(bi * 16 + 4 * q4 + r) * 64 + bj * 16 + l16] = -acc[r];
+          }
         }
       }
       __syncthreads();
