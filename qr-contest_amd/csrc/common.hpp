@@ -105,34 +105,26 @@ __device__ __forceinline__ void wave_argmax(float& babs, float& bv, int& bi) {
   bi = ri;
 }
 
-template <int CTRL>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
-  return ((uint64_t)hi << 32) | lo;
+// Wave-wide maximum of an unsigned 32-bit value (all 64 lanes active); the result is uniform.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)dpp_i<kDppQuad1032>((int)v));
+  v = max(v, (uint32_t)dpp_i<kDppQuad2301>((int)v));
+  v = max(v, (uint32_t)dpp_i<kDppRowHalfMirror>((int)v));
+  v = max(v, (uint32_t)dpp_i<kDppRowMirror>((int)v));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
 }
 
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-// Wave-wide maximum of an unsigned 64-bit key (all 64 lanes active); the result is uniform.
-// Four DPP butterflies reduce each row of 16 lanes, the four rows are combined by readlane.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  uint64_t o;
-  o = dpp_u64<kDppQuad1032>(v); v = o > v ? o : v;
-  o = dpp_u64<kDppQuad2301>(v); v = o > v ? o : v;
-  o = dpp_u64<kDppRowHalfMirror>(v); v = o > v ? o : v;
-  o = dpp_u64<kDppRowMirror>(v); v = o > v ? o : v;
-  uint64_t r = readlane_u64(v, 0);
-#pragma unroll
-  for (int row = 1; row < 4; ++row) {
-    const uint64_t t = readlane_u64(v, 16 * row);
-    r = t > r ? t : r;
-  }
-  return r;
+// Wave-wide maximum of a 64-bit key as two 32-bit reductions: the largest high word, then the
+// largest low word among the lanes that hold it (lexicographic order = unsigned 64-bit order).
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t key) {
+  const uint32_t hi = (uint32_t)(key >> 32), lo = (uint32_t)key;
+  const uint32_t mh = wave_max_u32(hi);
+  const uint32_t ml = wave_max_u32(hi == mh ? lo : 0u);
+  return ((uint64_t)mh << 32) | ml;
 }
 
 // Component I of a float4 (compile-time I).

@@ -192,7 +192,7 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
               const uint64_t key = ((uint64_t)kb32 << 32) | (uint32_t)(((2047 - pos[q]) << 4) | wid);
               if (key > best) { best = key; bq = q; }
             }
-            const uint64_t wbest = wave_max_u64(best);
+            const uint64_t wbest = wave_max_key(best);
             if (best == wbest) {  // exactly one lane: keys are distinct
               atomicMax(kcur, (unsigned long long)wbest);
               // the winning row by selects (a branch per row would be merged into a
