@@ -53,6 +53,19 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// An LDS float4 pointer in a register the compiler cannot see through: reads from it use
+// immediate offsets from that one register instead of one materialised address per read.
+typedef __attribute__((address_space(3))) const f32x4 lds_f4;
+__device__ __forceinline__ const lds_f4* lds_base(const float4* p) {
+  const lds_f4* q = (const lds_f4*)p;
+  asm volatile("" : "+v"(q));
+  return q;
+}
+__device__ __forceinline__ float4 lds_get(const lds_f4* p, int i) {
+  const f32x4 v = p[i];
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
 inline int lu_panel_nb(int n) { return n <= 512 ? 64 : (n <= 1024 ? 32 : 16); }
 
 // panel [n][nb+1] | -U12 chunk [nb][64] | row map [n] | pivot keys [3] (u64) | per-wave
@@ -219,8 +232,12 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
             const uint64_t pk = *kcur;
             const int pw = (int)(pk & 15u);
             const int p = 2047 - (int)((uint32_t)pk >> 4);
+            // one base register per column, the reads at immediate offsets from it (otherwise the
+            // compiler forms one address per read, hoisted out of the panel loop and parked in
+            // spilled registers)
+            const lds_f4* prow = lds_base(sb + pw * SLOT4 + 1);
 #pragma unroll
-            for (int c4 = C0; c4 < NB4; ++c4) pr4[c4 - C0] = sb[pw * SLOT4 + 1 + c4];
+            for (int c4 = C0; c4 < NB4; ++c4) pr4[c4 - C0] = lds_get(prow, c4);
             const float pv = f4get<j % 4>(pr4[0]);
             // LAPACK xGETRF2: scale by the reciprocal unless the pivot is subnormal; a zero
             // pivot leaves the column as it is (then every candidate is zero: no update)
@@ -252,8 +269,9 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
           }
           __syncthreads();
           if (wact) {
+            const lds_f4* prow = lds_base(sb + 1);  // one base register per column, as in the LU branch
 #pragma unroll
-            for (int c4 = C0; c4 < NB4; ++c4) pr4[c4 - C0] = sb[1 + c4];
+            for (int c4 = C0; c4 < NB4; ++c4) pr4[c4 - C0] = lds_get(prow, c4);
             const float d = f4get<j % 4>(pr4[0]);
             const float pp = 1.f - d, pm = 1.f + d;
             const bool plus = fabsf(pp) >= fabsf(pm);  // |1-d| >= |1+d|: the tie d = 0 takes +1
