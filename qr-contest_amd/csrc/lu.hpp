@@ -105,7 +105,7 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
   if (PIVOT)
     for (int i = tid; i < n; i += T) pl[i] = (SPLIT && a.k0 > 0) ? a.perm[(int64_t)b * n + i] : i;
   if (tid < 3) pkeys[tid] = 0ull;
-  int step = 0;  // LU column steps so far (selects the pivot key buffer)
+  int kb3 = 0;  // pivot key buffer of this LU column step: steps so far mod 3 (a rotating counter)
   __syncthreads();
 
   for (int k0 = SPLIT ? a.k0 : 0; k0 < n; k0 += NB) {
@@ -190,9 +190,10 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
           // smaller position (LAPACK's first maximum); the low 4 bits name the wave.  Key
           // buffer = step mod 3; the next step's buffer is cleared now (its last readers
           // finished two barriers ago).
-          unsigned long long* kcur = pkeys + step % 3;
-          if (tid == 0) pkeys[(step + 1) % 3] = 0ull;
-          ++step;
+          const int kb3n = kb3 == 2 ? 0 : kb3 + 1;
+          unsigned long long* kcur = pkeys + kb3;
+          if (tid == 0) pkeys[kb3n] = 0ull;
+          kb3 = kb3n;
           if (wact) {
             uint64_t best = 0;
             int bq = 0;
