@@ -85,8 +85,9 @@ __device__ __forceinline__ int chol_diag_wave(float* D, float* RT, float* RI, fl
     wave_lds_order();
     if constexpr (C0 < 16) {
       float4 p[16 - C0];
+      const lds_f4* sbp = lds_base(SB);
 #pragma unroll
-      for (int c4 = C0; c4 < 16; ++c4) p[c4 - C0] = reinterpret_cast<const float4*>(SB)[c4];
+      for (int c4 = C0; c4 < 16; ++c4) p[c4 - C0] = lds_get(sbp, c4);
 #pragma unroll
       for (int c4 = C0; c4 < 16; ++c4) {
         const float pv[4] = {p[c4 - C0].x, p[c4 - C0].y, p[c4 - C0].z, p[c4 - C0].w};
@@ -122,9 +123,10 @@ __device__ __forceinline__ void chol_inverse_wave(const float* RT, const float* 
   static_for<0, 64>([&](auto cc) {
     constexpr int c = decltype(cc)::value;
     float acc = (lane == c) ? 1.f : 0.f;
+    const lds_f4* rtc = lds_base(RT + c * 68);
 #pragma unroll
     for (int k4 = 0; k4 < (c + 3) / 4; ++k4) {
-      const float4 rv = reinterpret_cast<const float4*>(RT + c * 68)[k4];
+      const float4 rv = lds_get(rtc, k4);
       const float rvv[4] = {rv.x, rv.y, rv.z, rv.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e)

@@ -127,6 +127,24 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t key) {
   return ((uint64_t)mh << 32) | ml;
 }
 
+// An LDS float4 pointer in a register the compiler cannot see through: reads from it use
+// immediate offsets from that one register instead of one materialised (and hoisted) address
+// per read.
+typedef float lds_v4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) const lds_v4_t lds_f4;
+__device__ __forceinline__ const lds_f4* lds_base(const float* p) {
+  const lds_f4* q = (const lds_f4*)p;
+  asm volatile("" : "+v"(q));
+  return q;
+}
+__device__ __forceinline__ const lds_f4* lds_base(const float4* p) {
+  return lds_base(reinterpret_cast<const float*>(p));
+}
+__device__ __forceinline__ float4 lds_get(const lds_f4* p, int i) {
+  const lds_v4_t v = p[i];
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
 // Component I of a float4 (compile-time I).
 template <int I>
 __device__ __forceinline__ float f4get(const float4& v) {

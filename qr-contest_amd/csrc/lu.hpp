@@ -53,19 +53,6 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// An LDS float4 pointer in a register the compiler cannot see through: reads from it use
-// immediate offsets from that one register instead of one materialised address per read.
-typedef __attribute__((address_space(3))) const f32x4 lds_f4;
-__device__ __forceinline__ const lds_f4* lds_base(const float4* p) {
-  const lds_f4* q = (const lds_f4*)p;
-  asm volatile("" : "+v"(q));
-  return q;
-}
-__device__ __forceinline__ float4 lds_get(const lds_f4* p, int i) {
-  const f32x4 v = p[i];
-  return make_float4(v[0], v[1], v[2], v[3]);
-}
-
 inline int lu_panel_nb(int n) { return n <= 512 ? 64 : (n <= 1024 ? 32 : 16); }
 
 // panel [n][nb+1] | -U12 chunk [nb][64] | row map [n] | pivot keys [3] (u64) | per-wave
