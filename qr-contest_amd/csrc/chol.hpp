@@ -37,7 +37,7 @@ constexpr int kCholNb = 64;
 
 inline size_t chol_lds_bytes(int n, bool strip) {
   const size_t w = n > kCholNb ? (size_t)(n - kCholNb) : 1;
-  return sizeof(float) * (64 * 65 + 64 * 68 + 64 + 64 + 32 + (strip ? 64 * w : 0));
+  return sizeof(float) * (64 * 65 + 64 * 68 + 64 + 64 + 32 + (strip ? 64 * w + 64 : 0));
 }
 
 // Wave 0: factor the 64x64 diagonal block held in D (symmetric; the upper part is read) in
@@ -250,25 +250,30 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
               acc[mi][nj][r] = (row < n && col < n) ? G[row * n + col] : 0.f;
             }
         if (!first) {
-#pragma unroll 4
-          for (int kk = 0; kk < kCholNb; kk += 2) {
-            const int k = kk + h;
-            float av[2], bv[2];
+          // Operand reads are unconditional: a row ci >= w of R_k,> only meets accumulator
+          // rows (or columns) >= w of this tile, which are never stored.  The strip has 64
+          // floats of padding for that, and in G such reads stay inside the matrix (k1 < n).
+          const int ci0 = I * 64 + l32, cj0 = J * 64 + l32;
+          if (a.strip_lds) {
+#pragma unroll 8
+            for (int kk = 0; kk < kCholNb; kk += 2) {
+              const float* sk = S + (kk + h) * lds_w;
+              const float av[2] = {-sk[ci0], -sk[ci0 + 32]}, bv[2] = {sk[cj0], sk[cj0 + 32]};
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              const int ci = I * 64 + q * 32 + l32, cj = J * 64 + q * 32 + l32;
-              if (a.strip_lds) {
-                av[q] = (ci < w) ? -S[k * lds_w + ci] : 0.f;
-                bv[q] = (cj < w) ? S[k * lds_w + cj] : 0.f;
-              } else {
-                av[q] = (ci < w) ? -G[(k0 + k) * n + k1 + ci] : 0.f;
-                bv[q] = (cj < w) ? G[(k0 + k) * n + k1 + cj] : 0.f;
-              }
+              for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = mfma(av[mi], bv[nj], acc[mi][nj]);
             }
+          } else {
+#pragma unroll 8
+            for (int kk = 0; kk < kCholNb; kk += 2) {
+              const float* gk = G + (k0 + kk + h) * n + k1;
+              const float av[2] = {-gk[ci0], -gk[ci0 + 32]}, bv[2] = {gk[cj0], gk[cj0 + 32]};
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
+              for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-              for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = mfma(av[mi], bv[nj], acc[mi][nj]);
+                for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = mfma(av[mi], bv[nj], acc[mi][nj]);
+            }
           }
         }
         if (pr == 0) {
