@@ -392,7 +392,7 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
           for (int t = 0; t < NB4; ++t) {
             const int k = 4 * t + q4;
             const int pr = PIVOT ? pl[k0 + k] : k0 + k;
-            bv[u][t] = (job < NJOB && col < n) ? cur[(int64_t)pr * n + col] : 0.f;
+            bv[u][t] = (job < NJOB) ? cur[(int64_t)pr * n + min(col, n - 1)] : 0.f;  // columns past n: unstored
           }
         }
 #pragma unroll
@@ -411,29 +411,35 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
       }
       __syncthreads();
 
-      // A22[:, chunk] += L21 (-U12): one 32-row tile per wave at a time
+      // A22[:, chunk] += L21 (-U12): one 32-row tile per wave at a time.  The loads are
+      // branch-free: rows / columns past n are clamped (their accumulator entries are not
+      // stored), so the row-map reads and the loads issue as one batch; panel rows past m
+      // are read as they are (stale rows inside the LDS allocation, again only reaching
+      // unstored accumulator rows).
       const int ntr = (n - k1 + 31) >> 5;
       for (int tr = wid; tr < ntr; tr += NW) {
         const int r0 = k1 + tr * 32;
+        int ln = lane;  // laundered per tile: the row offsets are formed here, not kept live
+        asm volatile("" : "+v"(ln));
+        const int l32 = ln & 31, h = ln >> 5;
+        int prw[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rw = min(r0 + acc_row(r, ln), n - 1);
+          prw[r] = PIVOT ? pl[rw] : rw;
+        }
+        const int colc0 = min(c0 + l32, n - 1), colc1 = min(c0 + 32 + l32, n - 1);
         f32x16 c[2];
 #pragma unroll
-        for (int nj = 0; nj < 2; ++nj)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int rw = r0 + acc_row(r, lane), col = c0 + nj * 32 + l32;
-            float v = 0.f;
-            if (rw < n && col < n) {
-              const int pr = PIVOT ? pl[rw] : rw;
-              v = cur[(int64_t)pr * n + col];
-            }
-            c[nj][r] = v;
-          }
+        for (int r = 0; r < 16; ++r) {
+          c[0][r] = cur[(int64_t)prw[r] * n + colc0];
+          c[1][r] = cur[(int64_t)prw[r] * n + colc1];
+        }
         const int lr = r0 - k0 + l32;
-        const bool in = lr < m;
 #pragma unroll
         for (int kk = 0; kk < NB; kk += 2) {
           const int k = kk + h;
-          const float av = in ? P[sw(lr, k)] : 0.f;
+          const float av = P[sw(lr, k)];
           c[0] = mfma(av, U[k * 64 + l32], c[0]);
           c[1] = mfma(av, U[k * 64 + 32 + l32], c[1]);
         }
@@ -441,11 +447,8 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
         for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int rw = r0 + acc_row(r, lane), col = c0 + nj * 32 + l32;
-            if (rw < n && col < n) {
-              const int pr = PIVOT ? pl[rw] : rw;
-              dst[(int64_t)pr * n + col] = c[nj][r];
-            }
+            const int rw = r0 + acc_row(r, ln), col = c0 + nj * 32 + l32;
+            if (rw < n && col < n) dst[(int64_t)prw[r] * n + col] = c[nj][r];
           }
       }
       __syncthreads();
