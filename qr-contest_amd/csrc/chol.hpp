@@ -199,10 +199,10 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
         asm volatile("" : "+v"(ln));
         const int l32 = ln & 31, h = ln >> 5;
         const int colr = job * 32 + l32, col = k1 + colr;
-        const int base = (k0 + h) * n + col;
+        const int base = (k0 + h) * n + min(col, n - 1);  // columns past n: computed, not stored
         float bv[32];
 #pragma unroll
-        for (int t = 0; t < 32; ++t) bv[t] = (col < n) ? G[base + 2 * t * n] : 0.f;
+        for (int t = 0; t < 32; ++t) bv[t] = G[base + 2 * t * n];
         f32x16 acc0 = zero16(), acc1 = zero16();
 #pragma unroll
         for (int t = 0; t < 32; ++t) {
@@ -244,10 +244,10 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
 #pragma unroll
           for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int row = k1 + I * 64 + mi * 32 + acc_row(r, ln);
-              const int col = k1 + J * 64 + nj * 32 + l32;
-              acc[mi][nj][r] = (row < n && col < n) ? G[row * n + col] : 0.f;
+            for (int r = 0; r < 16; ++r) {  // rows / columns past n clamped: never stored
+              const int row = min(k1 + I * 64 + mi * 32 + acc_row(r, ln), n - 1);
+              const int col = min(k1 + J * 64 + nj * 32 + l32, n - 1);
+              acc[mi][nj][r] = G[row * n + col];
             }
         if (!first) {
           // Operand reads are unconditional: a row ci >= w of R_k,> only meets accumulator
@@ -394,10 +394,10 @@ __global__ __launch_bounds__(kCholSplitThreads) void k_chol_row(CholSplitArgs a)
   __syncthreads();
   if (32 * job >= w) return;
   const int colr = job * 32 + l32, col = k1 + colr;
-  const int base = (k0 + h) * n + col;
+  const int base = (k0 + h) * n + min(col, n - 1);  // columns past n: computed, not stored
   float bv[32];
 #pragma unroll
-  for (int t = 0; t < 32; ++t) bv[t] = (col < n) ? G[base + 2 * t * n] : 0.f;
+  for (int t = 0; t < 32; ++t) bv[t] = G[base + 2 * t * n];
   f32x16 acc0 = zero16(), acc1 = zero16();
 #pragma unroll
   for (int t = 0; t < 32; ++t) {
@@ -433,21 +433,16 @@ __global__ __launch_bounds__(kCholSplitThreads) void k_chol_trail(CholSplitArgs 
 #pragma unroll
     for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = k1 + I * 64 + mi * 32 + acc_row(r, lane);
-        const int col = k1 + J * 64 + nj * 32 + l32;
-        acc[mi][nj][r] = (row < n && col < n) ? G[row * n + col] : 0.f;
+      for (int r = 0; r < 16; ++r) {  // rows / columns past n clamped: never stored
+        const int row = min(k1 + I * 64 + mi * 32 + acc_row(r, lane), n - 1);
+        const int col = min(k1 + J * 64 + nj * 32 + l32, n - 1);
+        acc[mi][nj][r] = G[row * n + col];
       }
-#pragma unroll 4
+  const int ci0 = I * 64 + l32, cj0 = J * 64 + l32;  // reads past w reach unstored entries only
+#pragma unroll 8
   for (int kk = 0; kk < kCholNb; kk += 2) {
-    const int k = kk + h;
-    float av[2], bv[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int ci = I * 64 + q * 32 + l32, cj = J * 64 + q * 32 + l32;
-      av[q] = (ci < w) ? -G[(k0 + k) * n + k1 + ci] : 0.f;
-      bv[q] = (cj < w) ? G[(k0 + k) * n + k1 + cj] : 0.f;
-    }
+    const float* gk = G + (k0 + kk + h) * n + k1;
+    const float av[2] = {-gk[ci0], -gk[ci0 + 32]}, bv[2] = {gk[cj0], gk[cj0 + 32]};
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
