@@ -508,7 +508,7 @@ __global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail(LuArgs a, int nchu
 #pragma unroll
       for (int t = 0; t < NB4; ++t) {
         const int k = 4 * t + q4;
-        const float bv = (col < n) ? cur[pls[k0 + k] * n + col] : 0.f;
+        const float bv = cur[pls[k0 + k] * n + min(col, n - 1)];  // columns past n: not stored
         acc = mfma16(Xs[bi * 16 + l16][k], bv, acc);
       }
 #pragma unroll
@@ -521,9 +521,9 @@ __global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail(LuArgs a, int nchu
   for (int tr = rg * (kLuTrailRows / 32) + wid; tr < ntr; tr += NW) {
     const int r0 = k1 + tr * 32;
     // L21 rows r0 .. r0 + 31 (columns k0 .. k1) into this wave's tile
-    for (int idx = lane; idx < 32 * NB; idx += 64) {
-      const int rr = idx / NB, k = idx - rr * NB, rw = r0 + rr;
-      Ls[wid][rr][k] = (rw < n) ? dst[pls[rw] * n + k0 + k] : 0.f;
+    for (int idx = lane; idx < 32 * NB; idx += 64) {  // rows past n clamped: never stored
+      const int rr = idx / NB, k = idx - rr * NB, rw = min(r0 + rr, n - 1);
+      Ls[wid][rr][k] = dst[pls[rw] * n + k0 + k];
     }
     wave_lds_order();
     f32x16 c[2];
@@ -531,8 +531,8 @@ __global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail(LuArgs a, int nchu
     for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int rw = r0 + acc_row(r, lane), col = c0 + nj * 32 + l32;
-        c[nj][r] = (rw < n && col < n) ? cur[pls[rw] * n + col] : 0.f;
+        const int rw = min(r0 + acc_row(r, lane), n - 1), col = min(c0 + nj * 32 + l32, n - 1);
+        c[nj][r] = cur[pls[rw] * n + col];  // clamped rows / columns are not stored
       }
 #pragma unroll
     for (int kk = 0; kk < NB; kk += 2) {
