@@ -1,13 +1,13 @@
 // Right triangular solve Q = M R^-1 (R upper), batched, one 128-row block of one matrix per
 // 256-thread workgroup -- the solve_triangular of reflection_no_reflectors.py:77.
 //
-// With 64-column blocks, Dinv_c = R_cc^-1 and W[k][c] = R[k][c] Dinv_c (k < c; both written
-// by the Cholesky kernel), block column c of the solution is
+// With 64-column blocks, Dinv_c = R_cc^-1 and the negated W[k][c] = -R[k][c] Dinv_c (k < c;
+// both written after the Cholesky factor), block column c of the solution is
 //
-//     Q[:, c] = M[:, c] Dinv_c - sum_{k < c} Q[:, k] W[k][c],
+//     Q[:, c] = M[:, c] Dinv_c + sum_{k < c} Q[:, k] (-W[k][c]),
 //
-// one MFMA product over K = 64 (c + 1): the chunks k < c take -Q (this workgroup's own
-// earlier output, L2-resident) against W, the last chunk takes M against Dinv_c.  The result
+// one MFMA product over K = 64 (c + 1): the chunks k < c take Q (this workgroup's own
+// earlier output, L2-resident) against -W, the last chunk takes M against Dinv_c.  The result
 // leaves the accumulators straight for HBM -- no per-block transpose or second product.  Row
 // blocks are independent, so the whole solve is one launch with batch * n/128 workgroups.
 // Each wave owns 32 rows x 64 columns (two 32x32 MFMA accumulators); K is staged through
@@ -24,7 +24,7 @@ namespace rnr {
 struct TrsmArgs {
   const float* M;
   int64_t sm;
-  const float* Wm;    // W[k][c] blocks at their R positions (rows k < c of block column c)
+  const float* Wm;    // -W[k][c] blocks at their R positions (rows k < c of block column c)
   int64_t sw;
   const float* Dinv;  // [batch][n][64]
   float* Q;
@@ -43,13 +43,13 @@ struct WblkArgs {
   const float* R;     // upper factor, stride sr (only the blocks above the diagonal are read)
   int64_t sr;
   const float* Dinv;  // [batch][n][64]
-  float* Wm;          // out: W blocks at their R positions, stride sw
+  float* Wm;          // out: -W blocks at their R positions, stride sw
   int64_t sw;
   int n, ncol, total;
   int vec4;           // n % 4 == 0 and R 16-byte aligned (batch stride too)
 };
 
-// W[:c, c] = R[:c, c] Dinv_c for block column c >= 1 (64-wide blocks): one block column of
+// -W[:c, c] = -R[:c, c] Dinv_c for block column c >= 1 (64-wide blocks): one block column of
 // one matrix per 256-thread workgroup.  Dinv_c is staged in LDS once; each wave takes 32-row
 // strips of the rows above the diagonal block: the strip is read row-contiguously (16 lanes
 // per 64-float row, float4 each) into the wave's own LDS tile, then multiplied on
@@ -105,8 +105,8 @@ __global__ __launch_bounds__(256) void k_wblocks(WblkArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int64_t o = (int64_t)(32 * strip + acc_row(r, lane)) * n + c0 + l32;
-      if (c0 + l32 < n) W[o] = acc0[r];
-      if (c0 + 32 + l32 < n) W[o + 32] = acc1[r];
+      if (c0 + l32 < n) W[o] = -acc0[r];
+      if (c0 + 32 + l32 < n) W[o + 32] = -acc1[r];
     }
   }
 }
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   constexpr int RB = kTrsmRows, BK = 16, LDA = BK + 1;
   __shared__ __attribute__((aligned(16))) float smA[2 * RB * LDA];  // A chunk: RB rows x BK
   __shared__ __attribute__((aligned(16))) float smB[2 * BK * 64];   // B chunk: BK x 64
-  __shared__ int prow[RB];
+  __shared__ __attribute__((aligned(16))) int prow[RB];
   __shared__ int mrow[RB];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -136,55 +136,74 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   }
   __syncthreads();
 
-  // staging: A chunk = RB x BK floats (2 float4 per thread), B chunk = BK x 64 floats (1)
+  // staging: A chunk = RB x BK floats (2 float4 per thread), B chunk = BK x 64 floats (1).
+  // A chunk never straddles c0 (BK divides 64), so the -Q / M choice is uniform per chunk, and
+  // the loads are branch-free: rows past n read row 0 (prow / mrow hold 0 there) and columns
+  // past n read clamped ones -- such entries only reach rows or columns of the accumulators
+  // that are never stored -- except the K rows past n of the diagonal chunk, which meet B rows
+  // set to zero.  Each thread's two A rows are fixed, so their offsets stay in registers.
+  // The loads are used only by the LDS stores after the chunk's MFMAs, so nothing touches the
+  // loaded registers before then: the diagonal chunk's masks are applied in lstore.
   float ra[8], rb[4];
-  // element (i, k) of the A operand of chunk column k: -Q (k < c0) or M (k >= c0)
-  auto a_elem = [&](int i, int k, int c0) -> float {
-    const int row = r0 + i;
-    if (row >= n || k >= n) return 0.f;
-    if (k < c0) return -Q[(int64_t)prow[i] * n + k];
-    if (a.mperm) return (k < row) ? M[(int64_t)mrow[i] * n + k] : (k == row ? 1.f : 0.f);
-    return M[(int64_t)row * n + k];
-  };
+  const int ia0 = tid >> 2, ia1 = 64 + (tid >> 2), ca = 4 * (tid & 3);
+  const int qo0 = prow[ia0] * n, qo1 = prow[ia1] * n;
+  const int mo0 = mrow[ia0] * n, mo1 = mrow[ia1] * n;
+  const int kr = tid >> 4, cb = 4 * (tid & 15);
   auto gload = [&](int kc, int c0) {
+    const int k = kc + ca;
+    if (kc < c0) {  // Q (this workgroup's earlier output) against -W
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int idx = tid + 256 * p;
-      const int i = idx >> 2, ca = 4 * (idx & 3), k = kc + ca;
-      const int row = r0 + i;
-      if (VEC4 && row < n && k + 3 < n && (k < c0 ? k + 3 < c0 : !a.mperm)) {
-        const float* src = (k < c0) ? Q + (int64_t)prow[i] * n + k : M + (int64_t)row * n + k;
-        const float4 v = *reinterpret_cast<const float4*>(src);
-        const float s = (k < c0) ? -1.f : 1.f;
-        ra[4 * p] = s * v.x; ra[4 * p + 1] = s * v.y; ra[4 * p + 2] = s * v.z; ra[4 * p + 3] = s * v.w;
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) ra[4 * p + q] = a_elem(i, k + q, c0);
-      }
-    }
-    {
-      const int kr = tid >> 4, cb = 4 * (tid & 15), k = kc + kr, col = c0 + cb;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (k < n) {
-        if (k < c0) {
-          if (VEC4 && col + 3 < n) {
-            v = *reinterpret_cast<const float4*>(Wm + (int64_t)k * n + col);
-          } else {
-            v.x = (col < n) ? Wm[(int64_t)k * n + col] : 0.f;
-            v.y = (col + 1 < n) ? Wm[(int64_t)k * n + col + 1] : 0.f;
-            v.z = (col + 2 < n) ? Wm[(int64_t)k * n + col + 2] : 0.f;
-            v.w = (col + 3 < n) ? Wm[(int64_t)k * n + col + 3] : 0.f;
-          }
+      for (int p = 0; p < 2; ++p) {
+        const float* src = Q + (p ? qo1 : qo0) + k;  // k + 3 < c0 <= n
+        float4 v;
+        if (VEC4) {
+          v = *reinterpret_cast<const float4*>(src);
         } else {
-          v = *reinterpret_cast<const float4*>(Dv + (int64_t)k * 64 + cb);  // zero past the block
+          v = make_float4(src[0], src[1], src[2], src[3]);
         }
+        ra[4 * p] = v.x; ra[4 * p + 1] = v.y; ra[4 * p + 2] = v.z; ra[4 * p + 3] = v.w;
       }
+      const float* wrow = Wm + (kc + kr) * n;  // kc + kr < c0
+      const int col = c0 + cb;
+      float4 v;
+      if (VEC4) {
+        v = *reinterpret_cast<const float4*>(wrow + min(col, n - 4));
+      } else {
+        v = make_float4(wrow[min(col, n - 1)], wrow[min(col + 1, n - 1)], wrow[min(col + 2, n - 1)],
+                        wrow[min(col + 3, n - 1)]);
+      }
+      rb[0] = v.x; rb[1] = v.y; rb[2] = v.z; rb[3] = v.w;
+    } else {  // the diagonal chunk: M (or the unit-lower view of L) against Dinv_c
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const float* mr = M + (p ? mo1 : mo0);
+        float4 v;
+        if (VEC4) {
+          v = *reinterpret_cast<const float4*>(mr + min(k, n - 4));
+        } else {
+          v = make_float4(mr[min(k, n - 1)], mr[min(k + 1, n - 1)], mr[min(k + 2, n - 1)], mr[min(k + 3, n - 1)]);
+        }
+        ra[4 * p] = v.x; ra[4 * p + 1] = v.y; ra[4 * p + 2] = v.z; ra[4 * p + 3] = v.w;
+      }
+      const float4 v = *reinterpret_cast<const float4*>(Dv + min(kc + kr, n - 1) * 64 + cb);  // zero past the block
       rb[0] = v.x; rb[1] = v.y; rb[2] = v.z; rb[3] = v.w;
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, int kc, int c0) {
     float* As = smA + buf * RB * LDA;
     float* Bs = smB + buf * BK * 64;
+    if (kc >= c0) {  // uniform: the diagonal chunk
+      if (a.mperm) {  // L[row][k]: stored below the diagonal, 1 on it, 0 above
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          int d = r0 + (p ? ia1 : ia0) - (kc + ca);  // row - k
+          asm volatile("" : "+v"(d));  // keeps the selects here instead of hoisted out of the loops
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ra[4 * p + q] = (q < d) ? ra[4 * p + q] : (q == d ? 1.f : 0.f);
+        }
+      }
+      if (kc + kr >= n) rb[0] = rb[1] = rb[2] = rb[3] = 0.f;  // K rows past n
+    }
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       const int idx = tid + 256 * p;
@@ -200,7 +219,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     f32x16 acc[2] = {zero16(), zero16()};
     int buf = 0;
     gload(0, c0);
-    lstore(0);
+    lstore(0, 0, c0);
     __syncthreads();
     for (int kc = 0; kc < kend; kc += BK) {
       const bool more = kc + BK < kend;
@@ -214,21 +233,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
         acc[0] = mfma(av, Bs[k * 64 + l32], acc[0]);
         acc[1] = mfma(av, Bs[k * 64 + 32 + l32], acc[1]);
       }
-      if (more) lstore(buf ^ 1);
+      if (more) lstore(buf ^ 1, kc + BK, c0);
       __syncthreads();
       buf ^= 1;
     }
+    // accumulator registers 4g .. 4g + 3 hold the consecutive rows wr + 8g + 4h + (0..3):
+    // their targets come from one 16-byte LDS read; full tiles store without masks
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    auto store_tile = [&](float* dst, auto masked) {
 #pragma unroll
-    for (int nj = 0; nj < 2; ++nj)
+      for (int g = 0; g < 4; ++g) {
+        const int lb = wr + 8 * g + 4 * (ln >> 5);
+        const int4 pr = *reinterpret_cast<const int4*>(&prow[lb]);
+        const int prr[4] = {pr.x, pr.y, pr.z, pr.w};
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lrow = wr + acc_row(r, lane), col = c0 + nj * 32 + l32;
-        if (r0 + lrow < n && col < n) {
-          const int64_t off = (int64_t)prow[lrow] * n + col;
-          Q[off] = acc[nj][r];
-          if (Q2) Q2[off] = acc[nj][r];
-        }
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int nj = 0; nj < 2; ++nj) {
+            const int col = c0 + nj * 32 + (ln & 31);
+            if (!decltype(masked)::value || (r0 + lb + q < n && col < n)) dst[prr[q] * n + col] = acc[nj][4 * g + q];
+          }
       }
+    };
+    if (r0 + RB <= n && c0 + 64 <= n) {  // uniform
+      store_tile(Q, std::false_type{});
+      if (Q2) store_tile(Q2, std::false_type{});
+    } else {
+      store_tile(Q, std::true_type{});
+      if (Q2) store_tile(Q2, std::true_type{});
+    }
     // the next block column reads these outputs back (other threads of this workgroup)
     __syncthreads();
   }
