@@ -71,80 +71,80 @@ __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
     lp = lps;
   }
   // element (r, c) of the unit-lower view: below the diagonal from row lp[r], 1 on it, 0 above
-  auto lview4 = [&](int gr, int c) -> float4 {
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (c < gr) v = *reinterpret_cast<const float4*>(X + (int64_t)lp[gr] * n + c);
-    v.x = (c < gr) ? v.x : (c == gr ? 1.f : 0.f);
-    v.y = (c + 1 < gr) ? v.y : (c + 1 == gr ? 1.f : 0.f);
-    v.z = (c + 2 < gr) ? v.z : (c + 2 == gr ? 1.f : 0.f);
-    v.w = (c + 3 < gr) ? v.w : (c + 3 == gr ? 1.f : 0.f);
-    return v;
-  };
   auto lview1 = [&](int gr, int c) -> float {
     return (c < gr) ? X[(int64_t)lp[gr] * n + c] : (c == gr ? 1.f : 0.f);
   };
+  // float4 slots (VEC4): a thread's column is the same in every slot, since 256 is a multiple
+  // of BM / 4.  The loads are branch-free -- rows past n read row n - 1 and columns past n read
+  // clamped ones (those only reach accumulator entries that are never stored) -- and nothing
+  // touches the loaded registers before the LDS store after the chunk's MFMAs, which applies
+  // the unit-lower view's masks and zeroes the K rows past n, both under uniform conditions.
+  constexpr int RQ = 256 / (BM / 4);  // rows between a thread's slots
+  const int c4 = 4 * (tid % (BM / 4)), rq = tid / (BM / 4);
+  const int cx = min(i0 + c4, n - 4), cy = min(j0 + c4, n - 4);
   auto gload = [&](int k) {
-    if (lp) {
-      if constexpr (VEC4) {
-#pragma unroll
-        for (int p = 0; p < PER / 4; ++p) {
-          const int idx = tid + 256 * p;
-          const int row = idx / (BM / 4), c = 4 * (idx % (BM / 4));
-          const int gr = k + row;
-          float4 vx = make_float4(0.f, 0.f, 0.f, 0.f), vy = vx;
-          if (gr < n) {
-            if (i0 + c < n) vx = lview4(gr, i0 + c);
-            if (j0 + c < n) vy = lview4(gr, j0 + c);
-          }
-          rx[4 * p + 0] = vx.x; rx[4 * p + 1] = vx.y; rx[4 * p + 2] = vx.z; rx[4 * p + 3] = vx.w;
-          ry[4 * p + 0] = vy.x; ry[4 * p + 1] = vy.y; ry[4 * p + 2] = vy.z; ry[4 * p + 3] = vy.w;
-        }
-      } else {
-#pragma unroll
-        for (int p = 0; p < PER; ++p) {
-          const int idx = tid + 256 * p;
-          const int row = idx / BM, c = idx % BM;
-          const int gr = k + row;
-          rx[p] = (gr < n && i0 + c < n) ? lview1(gr, i0 + c) : 0.f;
-          ry[p] = (gr < n && j0 + c < n) ? lview1(gr, j0 + c) : 0.f;
-        }
-      }
-      return;
-    }
     if constexpr (VEC4) {
 #pragma unroll
       for (int p = 0; p < PER / 4; ++p) {
-        const int idx = tid + 256 * p;
-        const int row = idx / (BM / 4), c = 4 * (idx % (BM / 4));
-        const int gr = k + row;
-        float4 vx = make_float4(0.f, 0.f, 0.f, 0.f), vy = vx;
-        if (gr < n) {
-          if (i0 + c < n) vx = *reinterpret_cast<const float4*>(X + (int64_t)gr * n + i0 + c);
-          if (j0 + c < n) vy = *reinterpret_cast<const float4*>(Y + (int64_t)gr * n + j0 + c);
-        }
+        const int gr = min(k + rq + RQ * p, n - 1);
+        const int ro = (lp ? lp[gr] : gr) * n;
+        const float4 vx = *reinterpret_cast<const float4*>(X + ro + cx);
+        const float4 vy = *reinterpret_cast<const float4*>((lp ? X : Y) + ro + cy);
         rx[4 * p + 0] = vx.x; rx[4 * p + 1] = vx.y; rx[4 * p + 2] = vx.z; rx[4 * p + 3] = vx.w;
         ry[4 * p + 0] = vy.x; ry[4 * p + 1] = vy.y; ry[4 * p + 2] = vy.z; ry[4 * p + 3] = vy.w;
       }
-    } else {
+      return;
+    }
+    if (lp) {
 #pragma unroll
       for (int p = 0; p < PER; ++p) {
         const int idx = tid + 256 * p;
         const int row = idx / BM, c = idx % BM;
         const int gr = k + row;
-        rx[p] = (gr < n && i0 + c < n) ? X[(int64_t)gr * n + i0 + c] : 0.f;
-        ry[p] = (gr < n && j0 + c < n) ? Y[(int64_t)gr * n + j0 + c] : 0.f;
+        rx[p] = (gr < n && i0 + c < n) ? lview1(gr, i0 + c) : 0.f;
+        ry[p] = (gr < n && j0 + c < n) ? lview1(gr, j0 + c) : 0.f;
       }
+      return;
+    }
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int idx = tid + 256 * p;
+      const int row = idx / BM, c = idx % BM;
+      const int gr = k + row;
+      rx[p] = (gr < n && i0 + c < n) ? X[(int64_t)gr * n + i0 + c] : 0.f;
+      ry[p] = (gr < n && j0 + c < n) ? Y[(int64_t)gr * n + j0 + c] : 0.f;
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, int k) {
     if constexpr (VEC4) {
+      if (lp) {
+        // L[gr][col]: stored below the diagonal, 1 on it, 0 above (only chunks that reach the
+        // tile's columns have entries on or above the diagonal)
+        auto lmask = [&](float* r, int col0) {
+#pragma unroll
+          for (int p = 0; p < PER / 4; ++p) {
+            int d = k + rq + RQ * p - col0;  // gr - col
+            asm volatile("" : "+v"(d));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[4 * p + e] = (e < d) ? r[4 * p + e] : (e == d ? 1.f : 0.f);
+          }
+        };
+        if (k < i0 + BM) lmask(rx, i0 + c4);
+        if (k < j0 + BM) lmask(ry, j0 + c4);
+      }
+      if (k + BK > n) {
+#pragma unroll
+        for (int p = 0; p < PER / 4; ++p)
+          if (k + rq + RQ * p >= n)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rx[4 * p + e] = ry[4 * p + e] = 0.f;
+      }
 #pragma unroll
       for (int p = 0; p < PER / 4; ++p) {
-        const int idx = tid + 256 * p;
-        const int row = idx / (BM / 4), c = 4 * (idx % (BM / 4));
-        *reinterpret_cast<float4*>(&Xs[buf][row][c]) =
+        const int row = rq + RQ * p;
+        *reinterpret_cast<float4*>(&Xs[buf][row][c4]) =
             make_float4(rx[4 * p], rx[4 * p + 1], rx[4 * p + 2], rx[4 * p + 3]);
-        *reinterpret_cast<float4*>(&Ys[buf][row][c]) =
+        *reinterpret_cast<float4*>(&Ys[buf][row][c4]) =
             make_float4(ry[4 * p], ry[4 * p + 1], ry[4 * p + 2], ry[4 * p + 3]);
       }
     } else {
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
   const int klo = a.klo_from_j ? j0 : 0;
   int buf = 0;
   gload(klo);
-  lstore(0);
+  lstore(0, klo);
   __syncthreads();
   for (int kc = klo; kc < n; kc += BK) {
     const bool more = kc + BK < n;
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
 #pragma unroll
         for (int nj = 0; nj < NB; ++nj) acc[mi][nj] = mfma(av[mi], bv[nj], acc[mi][nj]);
     }
-    if (more) lstore(buf ^ 1);
+    if (more) lstore(buf ^ 1, kc + BK);
     __syncthreads();
     buf ^= 1;
   }
