@@ -113,17 +113,29 @@ __device__ __forceinline__ int chol_diag_wave(float* D, float* RT, float* RI, fl
 }
 
 // Wave 0: XT = (R^-1)^T (XT[i][k] = Dinv[k][i], row stride 65) for the upper R given column-
-// major in RT (row stride 68), with 1 / R[c][c] in RI.  Lane i forms row i of X = R^-1 from
-// X R = I column by column, X[i][c] = (delta_ic - sum_{k<c} X[i][k] R[k][c]) / R[c][c]; the
-// column of R is a float4 LDS broadcast.  Rows below the diagonal come out as exact zeros.
-// XT may alias RT: it is written only after the last read of RT.
-__device__ __forceinline__ void chol_inverse_wave(const float* RT, const float* RI, float* XT, int lane) {
+// major in RT (row stride 68) and row-major in D (row stride 65, zeros below the diagonal),
+// with 1 / R[c][c] in RI.  Blocked by 32 (LAPACK strtri's block form):
+//   * X11 = R11^-1 and X22 = R22^-1 at once, lane 32 d + i forming row i of block d from
+//     X R = I column by column, X[i][c] = (delta_ic - sum_{k<c} X[i][k] R[k][c]) / R[c][c]
+//     (the columns of R are float4 LDS reads; rows below the diagonal come out as exact zeros);
+//   * X12 = -X11 (R12 X22) on v_mfma_f32_32x32x2f32, R12 X22 staying in the accumulators and
+//     used from there as the B operand of the second product (register r of a 32x32
+//     accumulator holds rows 8(r/4) + r%4 and that + 4 in its two half-waves: a K = 2 pair).
+// XT aliases RT: the diagonal blocks are written only after the last read of RT, and the
+// products read R12 from D.
+__device__ __forceinline__ void chol_inverse_wave(const float* RT, const float* RI, const float* D, float* XT,
+                                                  int lane) {
   asm volatile("" : "+v"(lane));  // lane-derived values stay here, not hoisted out of the caller's loop
-  float x[64];
-  static_for<0, 64>([&](auto cc) {
+  const int l32 = lane & 31, h = lane >> 5, o = 32 * h;  // block h, row l32 within it
+  float x[32];
+  static_for<0, 32>([&](auto cc) {
     constexpr int c = decltype(cc)::value;
-    float acc = (lane == c) ? 1.f : 0.f;
-    const lds_f4* rtc = lds_base(RT + c * 68);
+    float acc = (l32 == c) ? 1.f : 0.f;
+    // the column's reads depend on x[c - 2]: they issue one column ahead, not all at the start
+    // (hoisted together they would not fit in registers)
+    int off = (o + c) * 68 + o, ri = o + c;
+    if constexpr (c >= 2) asm volatile("" : "+v"(off), "+v"(ri) : "v"(x[c - 2]));
+    const lds_f4* rtc = lds_base(RT + off);
 #pragma unroll
     for (int k4 = 0; k4 < (c + 3) / 4; ++k4) {
       const float4 rv = lds_get(rtc, k4);
@@ -132,12 +144,26 @@ __device__ __forceinline__ void chol_inverse_wave(const float* RT, const float* 
       for (int e = 0; e < 4; ++e)
         if (4 * k4 + e < c) acc -= x[4 * k4 + e] * rvv[e];
     }
-    x[c] = acc * RI[c];
-    __builtin_amdgcn_sched_barrier(0);
+    x[c] = acc * RI[ri];
   });
   wave_lds_order();
 #pragma unroll
-  for (int c = 0; c < 64; ++c) XT[c * 65 + lane] = x[c];
+  for (int c = 0; c < 32; ++c) {
+    XT[(o + c) * 65 + o + l32] = x[c];
+    if (h) XT[c * 65 + 32 + l32] = 0.f;  // X21
+  }
+  wave_lds_order();
+  f32x16 u = zero16();  // R12 X22
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    const int k = 2 * t + h;
+    u = mfma(D[l32 * 65 + 32 + k], XT[(32 + l32) * 65 + 32 + k], u);
+  }
+  f32x16 x12 = zero16();  // -X11 (R12 X22)
+#pragma unroll
+  for (int r = 0; r < 16; ++r) x12 = mfma(-XT[acc_row(r, lane) * 65 + l32], u[r], x12);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) XT[(32 + l32) * 65 + acc_row(r, lane)] = x12[r];
 }
 
 __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
@@ -292,7 +318,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
           const int fail = chol_diag_wave(D, RT, RI, SB, lane);
           if (lane == 0 && fail != INT_MAX && fail < kbn && *ffail == INT_MAX) *ffail = k1 + fail + 1;
           wave_lds_order();
-          chol_inverse_wave(RT, RI, XT, lane);
+          chol_inverse_wave(RT, RI, D, XT, lane);
         } else {
 #pragma unroll
           for (int mi = 0; mi < 2; ++mi)
@@ -352,7 +378,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol_jitter(CholSplitArgs a) {
 
 __global__ __launch_bounds__(64) void k_chol_diag(CholSplitArgs a) {
   __shared__ float D[64 * 65];
-  __shared__ float XT[64 * 68];  // RT while factoring, then XT
+  __shared__ __attribute__((aligned(16))) float XT[64 * 68];  // RT while factoring, then XT
   __shared__ float RI[64];
   __shared__ float SB[64];
   const int n = a.n, k0 = a.k0, b = blockIdx.x, lane = threadIdx.x;
@@ -367,7 +393,7 @@ __global__ __launch_bounds__(64) void k_chol_diag(CholSplitArgs a) {
   const int fail = chol_diag_wave(D, XT, RI, SB, lane);
   if (lane == 0 && fail != INT_MAX && fail < kb && a.info[b] == 0) a.info[b] = k0 + fail + 1;
   wave_lds_order();
-  chol_inverse_wave(XT, RI, XT, lane);
+  chol_inverse_wave(XT, RI, D, XT, lane);
   wave_lds_order();
   for (int idx = lane; idx < kb * 64; idx += 64) {
     const int i = idx >> 6, c = idx & 63;
