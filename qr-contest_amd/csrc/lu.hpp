@@ -67,6 +67,61 @@ inline size_t lu_lds_bytes(int n, int nb) {
 // which k_lu_trail runs over many workgroups (for batches too small to fill the GPU with one
 // workgroup per matrix).  The row map then lives in a.perm between launches and L11^-1 goes
 // to a.X.
+// One wave: X = L^-1 for the 64 x 64 unit-lower L11 of a panel, written over the panel's top
+// 64 rows P (row stride 65), with the strict lower part of L given transposed in LT
+// (LT[c][k] = L[k][c], row stride 64, zero for k <= c).  Blocked by 32:
+//   * X11 = L11^-1 and X22 = L22^-1 at once, lane 32 d + i forming row i of block d from
+//     X L = I column by column, last column first: X[i][c] = delta_ic - sum_{k>c} X[i][k] L[k][c]
+//     (the columns of L are float4 LDS reads; entries above the diagonal come out as exact
+//     zeros);
+//   * X21 = -X22 (L21 X11) on v_mfma_f32_32x32x2f32, L21 X11 staying in the accumulators and
+//     used from there as the B operand of the second product (register r of a 32x32
+//     accumulator holds rows 8(r/4) + r%4 and that + 4 in its two half-waves: a K = 2 pair).
+__device__ __forceinline__ void lu_inverse_wave(float* P, const float* LT, int lane) {
+  constexpr int LDP = 65;
+  asm volatile("" : "+v"(lane));  // lane-derived values stay here, not hoisted out of the caller's loop
+  const int l32 = lane & 31, h = lane >> 5, o = 32 * h;  // block h, row l32 within it
+  float x[32];
+  static_for<0, 32>([&](auto cc) {
+    constexpr int c = 31 - decltype(cc)::value;
+    float acc = (l32 == c) ? 1.f : 0.f;
+    if constexpr (c < 31) {
+      // the column's reads depend on x[c + 2]: they issue one column ahead, not all at the
+      // start (hoisted together they would not fit in registers)
+      int off = (o + c) * 64 + o;
+      if constexpr (c <= 29) asm volatile("" : "+v"(off) : "v"(x[c + 2]));
+      const lds_f4* lc = lds_base(LT + off);
+#pragma unroll
+      for (int k4 = (c + 1) / 4; k4 < 8; ++k4) {
+        const float4 lv = lds_get(lc, k4);
+        const float lvv[4] = {lv.x, lv.y, lv.z, lv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (4 * k4 + e > c) acc -= x[4 * k4 + e] * lvv[e];
+      }
+    }
+    x[c] = acc;
+  });
+  wave_lds_order();
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    P[(o + l32) * LDP + o + c] = x[c];
+    if (!h) P[l32 * LDP + 32 + c] = 0.f;  // X12
+  }
+  wave_lds_order();
+  f32x16 v = zero16();  // L21 X11
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    const int k = 2 * t + h;
+    v = mfma(LT[k * 64 + 32 + l32], P[k * LDP + l32], v);
+  }
+  f32x16 x21 = zero16();  // -X22 (L21 X11)
+#pragma unroll
+  for (int r = 0; r < 16; ++r) x21 = mfma(-P[(32 + l32) * LDP + 32 + acc_row(r, lane)], v[r], x21);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) P[(32 + acc_row(r, lane)) * LDP + l32] = x21[r];
+}
+
 template <bool PIVOT, int NB, int RPT, bool SPLIT = false>
 __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
   constexpr int T = kLuThreads, NW = T / 64;
@@ -342,9 +397,20 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
     }
     if (k1 >= n) break;  // uniform: no trailing matrix (and kb == NB below this line)
 
-    // ---- X = L11^-1 (unit lower) into panel rows 0..NB: wave w sweeps columns
-    //      w*CPW .. w*CPW+CPW-1, lane i holding row i; x_i -= L[i][k] x_k for i > k >= c.
-    {
+    // ---- X = L11^-1 (unit lower) into panel rows 0..NB
+    if constexpr (NB == 64) {
+      // L11^T (strict lower part) staged in the -U12 buffer, which is free until the trailing
+      // update; then one wave forms X by 32 x 32 blocks (lu_inverse_wave)
+      for (int idx = tid; idx < 64 * 64; idx += T) {
+        const int c = idx >> 6, k = idx & 63;
+        U[idx] = (k > c) ? P[sw(k, c)] : 0.f;
+      }
+      __syncthreads();
+      if (wid == 0) lu_inverse_wave(P, U, lane);
+      __syncthreads();
+    } else {
+      // wave w sweeps columns w*CPW .. w*CPW+CPW-1, lane i holding row i;
+      // x_i -= L[i][k] x_k for i > k >= c
       float Lr[NB];
 #pragma unroll
       for (int k = 0; k < NB; ++k) Lr[k] = (lane < NB && k < lane) ? P[sw(lane, k)] : 0.f;
