@@ -67,32 +67,41 @@ __global__ __launch_bounds__(256) void k_wblocks(WblkArgs a) {
   const float* Dv = a.Dinv + (int64_t)b * n * 64;
   float* W = a.Wm + b * a.sw;
   float* Rw = Rs[wid];
+  // strip rows 32 strip .. +31 (< c0 <= n), columns c0 .. c0 + 63: 4 rows per instruction.
+  // The first strip's loads issue before Dinv_c is staged, and each next strip's
+  // as soon as the current one is in LDS, under its MFMAs.
+  const int rq = lane >> 4, cq = 4 * (lane & 15), col = c0 + cq;
+  float4 v[8];
+  auto load_strip = [&](int strip) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float* src = R + (int64_t)(32 * strip + 4 * u + rq) * n + col;
+      if (a.vec4 && col + 3 < n) {
+        v[u] = *reinterpret_cast<const float4*>(src);
+      } else {
+        v[u].x = (col < n) ? src[0] : 0.f;
+        v[u].y = (col + 1 < n) ? src[1] : 0.f;
+        v[u].z = (col + 2 < n) ? src[2] : 0.f;
+        v[u].w = (col + 3 < n) ? src[3] : 0.f;
+      }
+    }
+  };
+  if (wid < 2 * c) load_strip(wid);
   for (int idx = tid; idx < 64 * 16; idx += 256) {
     const int k = idx >> 4, j4 = idx & 15;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (c0 + k < n) v = reinterpret_cast<const float4*>(Dv + (int64_t)(c0 + k) * 64)[j4];  // zero past the block
-    reinterpret_cast<float4*>(Ds + k * 64)[j4] = v;
+    float4 dv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c0 + k < n) dv = reinterpret_cast<const float4*>(Dv + (int64_t)(c0 + k) * 64)[j4];  // zero past the block
+    reinterpret_cast<float4*>(Ds + k * 64)[j4] = dv;
   }
   __syncthreads();
   for (int strip = wid; strip < 2 * c; strip += 4) {
-    // strip rows 32 strip .. +31 (< c0 <= n), columns c0 .. c0 + 63: 4 rows per instruction
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int rr = 4 * u + (lane >> 4), col = c0 + 4 * (lane & 15);
-      const float* src = R + (int64_t)(32 * strip + rr) * n + col;
-      float4 v;
-      if (a.vec4 && col + 3 < n) {
-        v = *reinterpret_cast<const float4*>(src);
-      } else {
-        v.x = (col < n) ? src[0] : 0.f;
-        v.y = (col + 1 < n) ? src[1] : 0.f;
-        v.z = (col + 2 < n) ? src[2] : 0.f;
-        v.w = (col + 3 < n) ? src[3] : 0.f;
-      }
-      float* d = Rw + rr * LDR + 4 * (lane & 15);
-      d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+      float* d = Rw + (4 * u + rq) * LDR + cq;
+      d[0] = v[u].x; d[1] = v[u].y; d[2] = v[u].z; d[3] = v[u].w;
     }
     wave_lds_order();
+    if (strip + 4 < 2 * c) load_strip(strip + 4);
     f32x16 acc0 = zero16(), acc1 = zero16();
 #pragma unroll
     for (int t = 0; t < 32; ++t) {
