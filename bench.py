@@ -47,8 +47,9 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_headline_256x512.md")
 PROFILE_SYMBOL = {"k_trsm": [("rnr::k_trsm<true>", 2)], "k_chol": [("rnr::k_chol", 2)],
                   "k_lu<true> (LU)": [("rnr::k_lu<true, 64, 1, false>", 1)],
                   "k_lu<false> (chart)": [("rnr::k_lu<false, 64, 1, false>", 1)],
-                  "k_tn_upper": [("rnr::k_tn_upper<128, false, false, true, 16>", 2),
-                                 ("rnr::k_tn_upper<128, true, true, true, 32>", 1)]}
+                  "k_tn_upper": [("rnr::k_tn_upper<128, false, false, true, 16, true>", 1),
+                                 ("rnr::k_tn_upper<128, false, false, true, 16, false>", 1),
+                                 ("rnr::k_tn_upper<128, true, true, true, 16, false>", 1)]}
 
 
 def measured_traffic(kernel: str):

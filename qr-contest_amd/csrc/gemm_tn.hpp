@@ -34,14 +34,16 @@ struct TnArgs {
   int klo_from_j;
 };
 
-template <int BM, bool MASK_LOWER, bool ROW_SCALE, bool VEC4, int BK = 32>
+// LV: the kernel may be given the unit-lower L view (a.lperm); without it the row map's LDS is
+// not allocated, which leaves room for more workgroups per CU.
+template <int BM, bool MASK_LOWER, bool ROW_SCALE, bool VEC4, int BK = 32, bool LV = true>
 __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
   constexpr int WM = BM / 2;
   constexpr int NB = WM / 32;
   constexpr int PER = BK * BM / 256;  // elements per thread per operand per chunk
   __shared__ __attribute__((aligned(16))) float Xs[2][BK][BM];
   __shared__ __attribute__((aligned(16))) float Ys[2][BK][BM];
-  __shared__ int lps[RNR_MAX_N];  // the row map of L (L view only)
+  __shared__ int lps[LV ? RNR_MAX_N : 1];  // the row map of L (L view only)
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5;
@@ -64,7 +66,7 @@ __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
   // the row map is staged in LDS once: every K chunk then looks its rows up there instead of
   // waiting on a dependent global load before the data load
   const int* lp = nullptr;
-  if (a.lperm) {
+  if (LV && a.lperm) {
     const int* g = a.lperm + (int64_t)b * n;
     for (int i = (a.klo_from_j ? j0 : 0) + tid; i < n; i += 256) lps[i] = g[i];
     __syncthreads();

@@ -171,17 +171,18 @@ int launch_tn(bool closure, const float* X, int64_t sx, const float* Y, int64_t 
   a.total = (int)total;
   const bool vec4 = (n % 4 == 0) && (sx % 4 == 0) && (sy % 4 == 0) && aligned(X, 16) && aligned(Y, 16);
   const dim3 grid((unsigned)total), block(256);
-#define RNR_TN(BMv, MASK, RS, V) k_tn_upper<BMv, MASK, RS, V><<<grid, block, 0, st>>>(a)
-  if (closure) {
-    if (big) { if (vec4) RNR_TN(128, true, true, true); else RNR_TN(128, true, true, false); }
-    else     { if (vec4) RNR_TN(64, true, true, true);  else RNR_TN(64, true, true, false); }
+#define RNR_TN(BMv, MASK, RS, V, BKv, LVv) k_tn_upper<BMv, MASK, RS, V, BKv, LVv><<<grid, block, 0, st>>>(a)
+  if (closure) {  // no L view: the row map's LDS is left out
+    if (big) { if (vec4) RNR_TN(128, true, true, true, 16, false); else RNR_TN(128, true, true, false, 32, false); }
+    else     { if (vec4) RNR_TN(64, true, true, true, 32, false);  else RNR_TN(64, true, true, false, 32, false); }
   } else if (big && vec4) {
     // the Grams: 16-row K chunks halve the LDS, so more workgroups per CU cover each tile's
-    // fixed load / store latency (the short K ranges of the Gram of L gain most)
-    k_tn_upper<128, false, false, true, 16><<<grid, block, 0, st>>>(a);
+    // fixed load / store latency (the short K ranges of the Gram of L gain most); the Gram of
+    // Q1 has no L view and leaves the row map out as well
+    if (lperm) RNR_TN(128, false, false, true, 16, true); else RNR_TN(128, false, false, true, 16, false);
   } else {
-    if (big) { if (vec4) RNR_TN(128, false, false, true); else RNR_TN(128, false, false, false); }
-    else     { if (vec4) RNR_TN(64, false, false, true);  else RNR_TN(64, false, false, false); }
+    if (big) { if (vec4) RNR_TN(128, false, false, true, 32, true); else RNR_TN(128, false, false, false, 32, true); }
+    else     { if (vec4) RNR_TN(64, false, false, true, 32, true);  else RNR_TN(64, false, false, false, 32, true); }
   }
 #undef RNR_TN
   return hip_status();
