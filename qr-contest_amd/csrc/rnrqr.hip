@@ -9,8 +9,9 @@
 //   5. k_tn_upper        G = Q1^T Q1                                            (:73)
 //   6. k_chol            G -> R_b, Dinv, info                                   (:74-76)
 //      k_wblocks         W for R_b -> the (now dead) LU buffer
-//   7. k_trsm            Q = P (Q1 R_b^-1) -> Qb and H (row scatter)            (:77,81)
-//   8. k_lu<false>       chart in place on H: tails Y, signs s, tau             (:139-174,192)
+//   7. k_trsm            Q = P (Q1 R_b^-1) -> Qb (row scatter)                   (:77,81)
+//   8. k_lu<false>       chart of Q, read from Qb, worked in H: tails Y, signs  (:139-174,192)
+//                        s, tau (Qb stays intact for the closure)
 //   9. k_tn_upper        H_upper = diag(s) triu(Q^T A), masked to j >= i         (:186,195)
 // rnr_qr_f32_timed records one caller event before each launch and one after the last.
 //
@@ -336,9 +337,11 @@ int qr_path(const float* A, int64_t batch, int64_t n, int64_t batch_stride, floa
   const int ni = (int)n;
   const int64_t nn = n * n;
   int* inf = info ? info : w.info;
-  if (int e = frame(A, batch_stride, w, w.Qb, H, inf, batch, ni, st, mk)) return e;
+  if (int e = frame(A, batch_stride, w, w.Qb, nullptr, inf, batch, ni, st, mk)) return e;
   if (int e = mk.mark(st)) return e;
-  if (int e = launch_lu(false, H, nn, H, nn, batch, ni, nullptr, nullptr, w.s, tau, w.Dinv, st)) return e;
+  // the chart's first panel step reads Q from Qb, everything after works in H (the entries of
+  // H it never writes, its U12 blocks, lie above the diagonal, which the closure overwrites)
+  if (int e = launch_lu(false, w.Qb, nn, H, nn, batch, ni, nullptr, nullptr, w.s, tau, w.Dinv, st)) return e;
   if (int e = mk.mark(st)) return e;
   if (int e = launch_tn(true, w.Qb, nn, A, batch_stride, H, nn, w.s, nullptr, batch, ni, false, st))
     return e;
