@@ -120,10 +120,17 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 
 // Wave-wide maximum of a 64-bit key as two 32-bit reductions: the largest high word, then the
 // largest low word among the lanes that hold it (lexicographic order = unsigned 64-bit order).
+// When one lane alone holds the largest high word (the usual case), its low word is read
+// directly; only ties run the second reduction.
 __device__ __forceinline__ uint64_t wave_max_key(uint64_t key) {
   const uint32_t hi = (uint32_t)(key >> 32), lo = (uint32_t)key;
   const uint32_t mh = wave_max_u32(hi);
-  const uint32_t ml = wave_max_u32(hi == mh ? lo : 0u);
+  const uint64_t holders = __ballot(hi == mh);  // uniform
+  uint32_t ml;
+  if (__popcll(holders) == 1)
+    ml = (uint32_t)__builtin_amdgcn_readlane((int)lo, __ffsll((long long)holders) - 1);
+  else
+    ml = wave_max_u32(hi == mh ? lo : 0u);
   return ((uint64_t)mh << 32) | ml;
 }
 
