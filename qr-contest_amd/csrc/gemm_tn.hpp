@@ -32,6 +32,7 @@ struct TnArgs {
   int ntiles;   // upper tiles per matrix
   int total;    // grid size
   int klo_from_j;
+  int lpt;      // klo_from_j with total % 8 == 0 and ntiles | total / 8: longest tiles first
 };
 
 // LV: the kernel may be given the unit-lower L view (a.lperm); without it the row map's LDS is
@@ -47,10 +48,26 @@ __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5;
-  const int pid = xcd_remap(blockIdx.x, a.total);
-  const int b = pid / a.ntiles;
-  int ti, tj;
-  upper_tile(pid - b * a.ntiles, a.nt, ti, tj);
+  int b, ti, tj;
+  if (a.lpt) {
+    // the Gram of L: a tile's K range is n - j0, so each XCD's matrices are dispatched tile by
+    // tile in column-major order (decreasing K) -- the short tiles fill the tail -- while the
+    // XCD keeps the same matrices (and their L2 sharing) as below
+    const int per = a.total / 8, mpx = per / a.ntiles, q = blockIdx.x >> 3;
+    const int tr = q / mpx;
+    b = (blockIdx.x & 7) * mpx + (q - tr * mpx);
+    int t = tr, j = 0;
+    while (t > j) {
+      t -= j + 1;
+      ++j;
+    }
+    ti = t;
+    tj = j;
+  } else {
+    const int pid = xcd_remap(blockIdx.x, a.total);
+    b = pid / a.ntiles;
+    upper_tile(pid - b * a.ntiles, a.nt, ti, tj);
+  }
   const int n = a.n, i0 = ti * BM, j0 = tj * BM;
   const float* X = a.X + b * a.sx;
   const float* Y = a.Y + b * a.sy;

@@ -170,6 +170,7 @@ int launch_tn(bool closure, const float* X, int64_t sx, const float* Y, int64_t 
   const int64_t total = batch * a.ntiles;
   if (total > INT32_MAX) return RNR_ERR_INVALID_ARG;
   a.total = (int)total;
+  a.lpt = (klo_from_j && total % 8 == 0 && (total / 8) % a.ntiles == 0) ? 1 : 0;
   const bool vec4 = (n % 4 == 0) && (sx % 4 == 0) && (sy % 4 == 0) && aligned(X, 16) && aligned(Y, 16);
   const dim3 grid((unsigned)total), block(256);
 #define RNR_TN(BMv, MASK, RS, V, BKv, LVv) k_tn_upper<BMv, MASK, RS, V, BKv, LVv><<<grid, block, 0, st>>>(a)
