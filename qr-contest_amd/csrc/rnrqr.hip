@@ -202,6 +202,7 @@ int launch_wblocks(const float* R, int64_t sr, const float* Dinv, float* Wm, int
   const int64_t total = batch * a.ncol;
   if (total > INT32_MAX) return RNR_ERR_INVALID_ARG;
   a.total = (int)total;
+  a.lpt = (total % 8 == 0 && (total / 8) % a.ncol == 0) ? 1 : 0;
   k_wblocks<<<dim3((unsigned)total), dim3(256), 0, st>>>(a);
   return hip_status();
 }

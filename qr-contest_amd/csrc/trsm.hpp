@@ -47,6 +47,7 @@ struct WblkArgs {
   int64_t sw;
   int n, ncol, total;
   int vec4;           // n % 4 == 0 and R 16-byte aligned (batch stride too)
+  int lpt;            // total % 8 == 0 and ncol | total / 8: largest block columns first
 };
 
 // -W[:c, c] = -R[:c, c] Dinv_c for block column c >= 1 (64-wide blocks): one block column of
@@ -61,8 +62,19 @@ __global__ __launch_bounds__(256) void k_wblocks(WblkArgs a) {
   __shared__ float Rs[4][32 * LDR];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5;
-  const int pid = xcd_remap(blockIdx.x, a.total);
-  const int b = pid / a.ncol, c = 1 + pid - b * a.ncol, n = a.n, c0 = 64 * c;
+  // block column c has 2c strips: each XCD's matrices are dispatched block column by block
+  // column, largest first, so the small ones fill the tail (same matrices per XCD as xcd_remap)
+  int b, c;
+  if (a.lpt) {
+    const int mpx = a.total / 8 / a.ncol, q = blockIdx.x >> 3, cr = q / mpx;
+    b = (blockIdx.x & 7) * mpx + (q - cr * mpx);
+    c = a.ncol - cr;
+  } else {
+    const int pid = xcd_remap(blockIdx.x, a.total);
+    b = pid / a.ncol;
+    c = 1 + pid - b * a.ncol;
+  }
+  const int n = a.n, c0 = 64 * c;
   const float* R = a.R + b * a.sr;
   const float* Dv = a.Dinv + (int64_t)b * n * 64;
   float* W = a.Wm + b * a.sw;
