@@ -150,12 +150,18 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
   int kb3 = 0;  // pivot key buffer of this LU column step: steps so far mod 3 (a rotating counter)
   __syncthreads();
 
+  // 64-wide panels: the trailing update's chunk of the next panel's columns runs last and is
+  // written straight into the LDS panel (it never makes the round trip through HBM)
+  constexpr bool kNextInLds = NB == 64 && !SPLIT;
+  bool preloaded = false;
   for (int k0 = SPLIT ? a.k0 : 0; k0 < n; k0 += NB) {
     const int kb = min(NB, n - k0), m = n - k0, k1 = k0 + kb;
     const float* cur = (k0 == 0) ? src : dst;
 
     // ---- panel HBM -> LDS, four float4 loads in flight per thread
-    if (a.vec4) {
+    if (preloaded) {
+      // already in P from the previous panel's trailing update
+    } else if (a.vec4) {
       const int tot = m * NB4;
       for (int f0 = tid; f0 < tot; f0 += 4 * T) {
         float4 v[4];
@@ -442,8 +448,12 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
       return;
     }
 
-    // ---- trailing update, 64 columns at a time
-    for (int c0 = k1; c0 < n; c0 += 64) {
+    // ---- trailing update, 64 columns at a time (the next panel's chunk last when it is kept)
+    const int nch = (n - k1 + 63) >> 6;
+    f32x16 kt0[2], kt1[2];  // the kept chunk's tiles (at most two per wave: n <= 512)
+    for (int it = 0; it < nch; ++it) {
+      const int c0 = k1 + 64 * (kNextInLds ? (it + 1) % nch : it);
+      const bool keep = kNextInLds && it == nch - 1;
       // -U12 = -(X A12[:, c0:c0+64]) as (NB/16) x 4 blocks of 16x16 spread over the waves
       {
         // a wave's jobs load their A12 columns first, then multiply: one load latency per
@@ -483,7 +493,7 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
       // are read as they are (stale rows inside the LDS allocation, again only reaching
       // unstored accumulator rows).
       const int ntr = (n - k1 + 31) >> 5;
-      for (int tr = wid; tr < ntr; tr += NW) {
+      for (int tr = wid, slot = 0; tr < ntr; tr += NW, ++slot) {
         const int r0 = k1 + tr * 32;
         int ln = lane;  // laundered per tile: the row offsets are formed here, not kept live
         asm volatile("" : "+v"(ln));
@@ -509,6 +519,11 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
           c[0] = mfma(av, U[k * 64 + l32], c[0]);
           c[1] = mfma(av, U[k * 64 + 32 + l32], c[1]);
         }
+        if (keep) {
+          if (slot == 0) { kt0[0] = c[0]; kt0[1] = c[1]; }
+          else { kt1[0] = c[0]; kt1[1] = c[1]; }
+          continue;
+        }
 #pragma unroll
         for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
@@ -518,7 +533,26 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
           }
       }
       __syncthreads();
+      if (keep) {
+        // every wave is past its reads of this panel: the kept tiles become the next panel,
+        // row at logical position k1 + r in P row r (columns past n zero, as the load writes)
+        for (int tr = wid, slot = 0; tr < ntr; tr += NW, ++slot) {
+          const int r0 = k1 + tr * 32;
+          int ln = lane;
+          asm volatile("" : "+v"(ln));
+          const int l32 = ln & 31;
+#pragma unroll
+          for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int rw = r0 + acc_row(r, ln), cc = nj * 32 + l32;
+              const float v = slot == 0 ? kt0[nj][r] : kt1[nj][r];
+              if (rw < n) P[sw(rw - k1, cc)] = (k1 + cc < n) ? v : 0.f;
+            }
+        }
+      }
     }
+    preloaded = kNextInLds;  // uniform; the next panel's load is skipped
   }
   __syncthreads();
 
