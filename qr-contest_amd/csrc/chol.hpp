@@ -176,6 +176,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
   float* SB = RI + 64;             // [64] scaled pivot row broadcast (wave 0)
   float* red = SB + 64;            // [16]
   int* ffail = reinterpret_cast<int*>(red + 16);
+  int* dcnt = ffail + 1;           // diagonal-tile quadrants written by waves 1 and 3, so far
   float* S = red + 32;             // block row [64][n-64] when strip_lds
 
   const int n = a.n, b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -191,7 +192,10 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
   if (lane == 0) red[wid] = part;
-  if (tid == 0) *ffail = INT_MAX;
+  if (tid == 0) {
+    *ffail = INT_MAX;
+    *dcnt = 0;
+  }
   __syncthreads();
   float tot = 0.f;
 #pragma unroll
@@ -258,7 +262,75 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
     {
       const int nt = (w + 63) >> 6, npairs = first ? 1 : nt * (nt + 1) / 2;
       const int t0 = wid == 0 ? 0 : wid, tstep = wid == 0 ? npairs : NW - 1;
+      const int kbn = min(kCholNb, w);
+      // one 32x32 quadrant (qi, qj) of the next diagonal tile, updated and written into D
+      // (identity past n)
+      auto diag_quadrant = [&](int qi, int qj) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int l32 = ln & 31, h = ln >> 5;
+        f32x16 q;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {  // rows / columns past n clamped: never stored
+          const int row = min(k1 + 32 * qi + acc_row(r, ln), n - 1);
+          const int col = min(k1 + 32 * qj + l32, n - 1);
+          q[r] = G[row * n + col];
+        }
+        const int ci = 32 * qi + l32, cj = 32 * qj + l32;
+        if (a.strip_lds) {
+#pragma unroll 8
+          for (int kk = 0; kk < kCholNb; kk += 2) {
+            const float* sk = S + (kk + h) * lds_w;
+            q = mfma(-sk[ci], sk[cj], q);
+          }
+        } else {
+#pragma unroll 8
+          for (int kk = 0; kk < kCholNb; kk += 2) {
+            const float* gk = G + (k0 + kk + h) * n + k1;
+            q = mfma(-gk[ci], gk[cj], q);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = 32 * qi + acc_row(r, ln), c = 32 * qj + l32;
+          D[i * 65 + c] = (i < kbn && c < kbn) ? q[r] : (i == c ? 1.f : 0.f);
+        }
+      };
+      // the next diagonal tile's quadrants (0,1) and (1,1) run on waves 1 and 3, other SIMDs
+      // than wave 0's, before their own tiles; its quadrant (1,0) lies below the diagonal,
+      // which the factor never reads
+      if (!first && (wid == 1 || wid == 3)) {
+        diag_quadrant(wid == 3 ? 1 : 0, 1);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) atomicAdd(dcnt, 1);
+      }
+      auto diag_factor = [&]() {
+        wave_lds_order();
+        const int fail = chol_diag_wave(D, RT, RI, SB, lane);
+        if (lane == 0 && fail != INT_MAX && fail < kbn && *ffail == INT_MAX) *ffail = k1 + fail + 1;
+        wave_lds_order();
+        chol_inverse_wave(RT, RI, D, XT, lane);
+      };
       for (int pr = t0; pr < npairs; pr += tstep) {
+        if (pr == 0 && !first) {
+          // wave 0: quadrant (0,0), then wait for the other two (a bounded wait: past the
+          // limit the block is reported as failed instead of hanging)
+          diag_quadrant(0, 0);
+          const int target = 2 * (k0 / kCholNb + 1);
+          for (int spin = 0;; ++spin) {
+            const int got = __builtin_amdgcn_readfirstlane(
+                __hip_atomic_load(dcnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+            if (got >= target) break;
+            if (spin > (1 << 20)) {
+              if (lane == 0 && *ffail == INT_MAX) *ffail = k1 + 1;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+          diag_factor();
+          continue;
+        }
         int I, J;
         upper_tile(pr, nt, I, J);
         int ln = lane;  // laundered per tile, as above
@@ -303,8 +375,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
           }
         }
         if (pr == 0) {
-          // next diagonal block -> D (identity past n), then factor and invert it
-          const int kbn = min(kCholNb, w);
+          // the first diagonal block (iteration k0 = -64: no update) -> D, then factor and invert it
 #pragma unroll
           for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -314,11 +385,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
                 const int i = mi * 32 + acc_row(r, ln), c = nj * 32 + l32;
                 D[i * 65 + c] = (i < kbn && c < kbn) ? acc[mi][nj][r] : (i == c ? 1.f : 0.f);
               }
-          wave_lds_order();
-          const int fail = chol_diag_wave(D, RT, RI, SB, lane);
-          if (lane == 0 && fail != INT_MAX && fail < kbn && *ffail == INT_MAX) *ffail = k1 + fail + 1;
-          wave_lds_order();
-          chol_inverse_wave(RT, RI, D, XT, lane);
+          diag_factor();
         } else {
 #pragma unroll
           for (int mi = 0; mi < 2; ++mi)
