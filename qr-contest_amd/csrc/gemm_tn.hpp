@@ -45,6 +45,7 @@ __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
   __shared__ __attribute__((aligned(16))) float Xs[2][BK][BM];
   __shared__ __attribute__((aligned(16))) float Ys[2][BK][BM];
   __shared__ int lps[LV ? RNR_MAX_N : 1];  // the row map of L (L view only)
+  __shared__ __attribute__((aligned(16))) float rss[ROW_SCALE ? BM : 1];  // the tile's row scales (ROW_SCALE only)
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5;
@@ -88,6 +89,11 @@ __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
     for (int i = (a.klo_from_j ? j0 : 0) + tid; i < n; i += 256) lps[i] = g[i];
     __syncthreads();
     lp = lps;
+  }
+  // row scales staged once, made visible by the barrier after the first chunk's LDS store (read
+  // per element in the epilogue they were a chain of dependent global loads)
+  if constexpr (ROW_SCALE) {
+    for (int i = tid; i < BM; i += 256) rss[i] = (i0 + i < n) ? a.rs[(int64_t)b * n + i0 + i] : 0.f;
   }
   // element (r, c) of the unit-lower view: below the diagonal from row lp[r], 1 on it, 0 above
   auto lview1 = [&](int gr, int c) -> float {
@@ -203,21 +209,30 @@ __global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
   }
 
   float* C = a.C + b * a.sc;
-  const float* rs = ROW_SCALE ? a.rs + (int64_t)b * n : nullptr;
+  // accumulator registers 4g .. 4g + 3 hold the consecutive rows wr + 8g + 4h + (0..3): their
+  // row scales are one float4 LDS read
 #pragma unroll
   for (int mi = 0; mi < NB; ++mi)
 #pragma unroll
-    for (int nj = 0; nj < NB; ++nj)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = i0 + wi0 + mi * 32 + acc_row(r, lane);
-        const int col = j0 + wj0 + nj * 32 + l32;
-        if (row < n && col < n && (!MASK_LOWER || col >= row)) {
-          float v = acc[mi][nj][r];
-          if (ROW_SCALE) v *= rs[row];
-          C[(int64_t)row * n + col] = v;
-        }
+    for (int g = 0; g < 4; ++g) {
+      const int lr0 = wi0 + mi * 32 + 8 * g + 4 * h;
+      float sc[4] = {1.f, 1.f, 1.f, 1.f};
+      if constexpr (ROW_SCALE) {
+        const float4 s4 = *reinterpret_cast<const float4*>(&rss[lr0]);
+        sc[0] = s4.x; sc[1] = s4.y; sc[2] = s4.z; sc[3] = s4.w;
       }
+#pragma unroll
+      for (int nj = 0; nj < NB; ++nj)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = i0 + lr0 + e, col = j0 + wj0 + nj * 32 + l32;
+          if (row < n && col < n && (!MASK_LOWER || col >= row)) {
+            float v = acc[mi][nj][4 * g + e];
+            if (ROW_SCALE) v *= sc[e];
+            C[(int64_t)row * n + col] = v;
+          }
+        }
+    }
 }
 
 }  // namespace rnr
