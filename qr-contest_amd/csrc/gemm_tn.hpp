@@ -38,7 +38,7 @@ struct TnArgs {
 // LV: the kernel may be given the unit-lower L view (a.lperm); without it the row map's LDS is
 // not allocated, which leaves room for more workgroups per CU.
 template <int BM, bool MASK_LOWER, bool ROW_SCALE, bool VEC4, int BK = 32, bool LV = true>
-__global__ __launch_bounds__(256) void k_tn_upper(TnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_tn_upper(TnArgs a) {
   constexpr int WM = BM / 2;
   constexpr int NB = WM / 32;
   constexpr int PER = BK * BM / 256;  // elements per thread per operand per chunk
