@@ -8,12 +8,13 @@
 //   * all waves form the block row R_k,> = Dinv_kk^T G_k,> on MFMA, each wave owning whole
 //     32-column strips; when it fits it is also kept in LDS for the trailing update
 //     (n <= 576), otherwise it is read back from G;
-//   * the trailing update G_>,> -= R_k,>^T R_k,> (upper 64x64 tiles, MFMA) is split: wave 0
-//     takes the first diagonal tile -- the next diagonal block -- keeps it in LDS, factors it
-//     (one symmetric row per lane in registers, the scaled pivot row broadcast through LDS
-//     inside the wave, no barriers) and forms its inverse (lane i computes row i of R^-1 by
-//     forward substitution over LDS broadcasts of R's columns), while waves 1..7 update the
-//     other tiles.  The sequential diagonal work thus runs under the trailing update.
+//   * the trailing update G_>,> -= R_k,>^T R_k,> (upper 64x64 tiles, MFMA) is split: the
+//     first diagonal tile -- the next diagonal block -- is updated into LDS by quadrants on
+//     waves 0, 1 and 3 (three SIMDs; its lower-left quadrant is never read), then wave 0
+//     factors it (one symmetric row per lane in registers, the scaled pivot row broadcast
+//     through LDS inside the wave, no barriers) and forms its inverse blocked by 32, while
+//     waves 1..7 update the other tiles.  The sequential diagonal work thus runs under the
+//     trailing update.
 // The diagonal-block inverses go to Dinv ([n][64] per matrix) for the triangular solve that
 // follows.  info records the first column whose pivot was not positive (1-based; NaN
 // counts as not positive).

@@ -18,19 +18,21 @@
 //     needs only the broadcast and one barrier;
 //   * the factored panel goes to LDS (row stride NB+1: conflict-free column reads, and a
 //     thread addresses its own row with one base register) and back to HBM;
-//   * X = L11^-1 is swept column by column inside each wave (readlane broadcasts, no
-//     barriers); per chunk of 64 trailing columns -U12 = -X A12 runs on 16x16x4 MFMA over
-//     all waves and A22 += L21 (-U12) on 32x32x2 MFMA, one 32-row tile per wave at a
-//     time.  Only A22 streams through HBM/L2.
+//   * X = L11^-1: for 64-wide panels blocked by 32 in one wave (lu_inverse_wave), otherwise
+//     swept column by column inside each wave (readlane broadcasts, no barriers); per chunk
+//     of 64 trailing columns -U12 = -X A12 runs on 16x16x4 MFMA over all waves and
+//     A22 += L21 (-U12) on 32x32x2 MFMA, one 32-row tile per wave at a time.  Only A22
+//     streams through HBM/L2; with 64-wide panels the chunk of the next panel's columns is
+//     updated last and written straight into the LDS panel.
 #pragma once
 #include "common.hpp"
 
 namespace rnr {
 
 struct LuArgs {
-  const float* src;  // data read by the first panel step (A for the LU, H for the chart)
+  const float* src;  // data read by the first panel step (A for the LU, Q for the chart)
   int64_t ss;
-  float* dst;        // working matrix (LU: workspace W; chart: H itself)
+  float* dst;        // working matrix (LU: workspace W; chart: H)
   int64_t sd;
   int n;
   int vec4;          // n % 4 == 0 and src, dst 16-byte aligned (batch strides too)
