@@ -59,8 +59,8 @@ inline int lu_panel_nb(int n) { return n <= 512 ? 64 : (n <= 1024 ? 32 : 16); }
 
 // panel [n][nb+1] | -U12 chunk [nb][64] | row map [n] | pivot keys [3] (u64) | per-wave
 // candidate slots [2][8][nb+4]
-inline size_t lu_lds_bytes(int n, int nb) {
-  const size_t p = ((size_t)n * (nb + 1) + 3) & ~(size_t)3;
+inline size_t lu_lds_bytes(int n, int nb, bool direct = false) {
+  const size_t p = ((size_t)(direct ? nb : n) * (nb + 1) + 3) & ~(size_t)3;
   const size_t pl = ((size_t)n + 3) & ~(size_t)3;
   return sizeof(float) * (p + (size_t)nb * 64 + pl + 8 + 2 * 8 * (size_t)(nb + 4));
 }
@@ -134,7 +134,11 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   const int n = a.n;
   float* P = smem;                                  // panel [n][NB+1]
-  float* U = P + (((size_t)n * LDP + 3) & ~(size_t)3);  // -U12 chunk [NB][64]
+  // DIRECT (split launches with 32-wide panels): the panel's rows go between HBM and registers
+  // directly and only its first NB logical rows (L11) are kept in P; the chart's tau then comes
+  // from k_chart_tau after the last panel
+  constexpr bool DIRECT = SPLIT && NB == 32;
+  float* U = P + (((size_t)(DIRECT ? NB : n) * LDP + 3) & ~(size_t)3);  // -U12 chunk [NB][64]
   int* pl = reinterpret_cast<int*>(U + NB * 64);    // logical -> physical row
   unsigned long long* pkeys =                       // [3] pivot keys (LU), by step mod 3
       reinterpret_cast<unsigned long long*>(reinterpret_cast<float*>(pl) + ((n + 3) & ~3));
@@ -161,8 +165,8 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
     const float* cur = (k0 == 0) ? src : dst;
 
     // ---- panel HBM -> LDS, four float4 loads in flight per thread
-    if (preloaded) {
-      // already in P from the previous panel's trailing update
+    if (preloaded || DIRECT) {
+      // already in P from the previous panel's trailing update (or loaded into registers below)
     } else if (a.vec4) {
       const int tot = m * NB4;
       for (int f0 = tid; f0 < tot; f0 += 4 * T) {
@@ -196,11 +200,33 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
     }
     __syncthreads();
     float row[RPT][NB];
+    if constexpr (DIRECT) {
 #pragma unroll
-    for (int q = 0; q < RPT; ++q) {
-      const int r = tid + T * q;
+      for (int q = 0; q < RPT; ++q) {
+        const int r = tid + T * q;
+        const int pr = (r < m) ? (PIVOT ? pl[k0 + r] : k0 + r) : 0;
+        const float* srow = cur + (int64_t)pr * n + k0;
+        if (a.vec4 && kb == NB) {
 #pragma unroll
-      for (int c = 0; c < NB; ++c) row[q][c] = (r < m) ? P[sw(r, c)] : 0.f;
+          for (int c4 = 0; c4 < NB4; ++c4) {
+            const float4 v = *reinterpret_cast<const float4*>(srow + 4 * c4);
+            row[q][4 * c4] = (r < m) ? v.x : 0.f;
+            row[q][4 * c4 + 1] = (r < m) ? v.y : 0.f;
+            row[q][4 * c4 + 2] = (r < m) ? v.z : 0.f;
+            row[q][4 * c4 + 3] = (r < m) ? v.w : 0.f;
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < NB; ++c) row[q][c] = (r < m && c < kb) ? srow[c] : 0.f;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < RPT; ++q) {
+        const int r = tid + T * q;
+#pragma unroll
+        for (int c = 0; c < NB; ++c) row[q][c] = (r < m) ? P[sw(r, c)] : 0.f;
+      }
     }
 
     // ---- factor the panel column by column (compile-time column index).  One barrier per
@@ -359,19 +385,35 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
     });
 
     // ---- registers -> LDS panel, each row at its logical position; the row map follows
+    //      (DIRECT: only L11's rows go to P, every row straight back to its row of HBM)
 #pragma unroll
     for (int q = 0; q < RPT; ++q) {
       const int r = tid + T * q;
       if (r < m) {
+        if (!DIRECT || pos[q] < NB) {
 #pragma unroll
-        for (int c = 0; c < NB; ++c) P[sw(pos[q], c)] = row[q][c];
+          for (int c = 0; c < NB; ++c) P[sw(pos[q], c)] = row[q][c];
+        }
+        if constexpr (DIRECT) {
+          float* drow = dst + (int64_t)(PIVOT ? phys[q] : k0 + r) * n + k0;
+          if (a.vec4 && kb == NB) {
+#pragma unroll
+            for (int c4 = 0; c4 < NB4; ++c4)
+              *reinterpret_cast<float4*>(drow + 4 * c4) =
+                  make_float4(row[q][4 * c4], row[q][4 * c4 + 1], row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
+          } else {
+#pragma unroll
+            for (int c = 0; c < NB; ++c)
+              if (c < kb) drow[c] = row[q][c];
+          }
+        }
         if (PIVOT) pl[k0 + pos[q]] = phys[q];
       }
     }
     if (!PIVOT && tid < kb) a.s[(int64_t)b * n + k0 + tid] = my_s;
     __syncthreads();
 
-    if constexpr (!PIVOT) {
+    if constexpr (!PIVOT && !DIRECT) {
       // tau of the panel's columns from the finished multipliers (rows below the diagonal)
       for (int c = tid >> 3; c < kb; c += T / 8) {
         const int sub = tid & 7;
@@ -385,8 +427,9 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
       }
     }
 
-    // ---- factored panel -> HBM (same physical rows it came from)
-    if (a.vec4) {
+    // ---- factored panel -> HBM (same physical rows it came from; DIRECT: done above)
+    if (DIRECT) {
+    } else if (a.vec4) {
       const int tot = m * NB4;
       for (int f = tid; f < tot; f += T) {
         const int r = f / NB4, c = 4 * (f - r * NB4);
@@ -568,6 +611,24 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
       }
     }
   }
+}
+
+// tau of the finished chart for the split form, tau_c = 2 / (1 + sum_{r > c} Y[r][c]^2)
+// (reflection_no_reflectors.py:192), summed in k_lu's in-panel order -- rows c + 1 + sub in
+// steps of 8, then the 8 lanes of a group -- so the values equal the fused kernel's bit for bit.
+// One 256-thread workgroup per 32 columns of one matrix.
+__global__ __launch_bounds__(256) void k_chart_tau(const float* H, int64_t sh, float* tau, int n, int ncb) {
+  const int64_t g = blockIdx.x, b = g / ncb;
+  const int c = (int)(g - b * ncb) * 32 + (threadIdx.x >> 3), sub = threadIdx.x & 7;
+  const float* Hb = H + b * sh;
+  float acc = 0.f;
+  if (c < n)
+    for (int r = c + 1 + sub; r < n; r += 8) {
+      const float y = Hb[(int64_t)r * n + c];
+      acc += y * y;
+    }
+  acc = group8_sum(acc);
+  if (sub == 0 && c < n) tau[b * n + c] = 2.f / (acc + 1.f);
 }
 
 // Trailing update of panel a.k0 for SPLIT launches: one 256-thread workgroup per (64-column

@@ -118,7 +118,7 @@ bool lu_split(int64_t batch, int n) { return n > 512 && batch < 128; }
 
 template <bool PIVOT, int NB, int RPT>
 int launch_lu_split(LuArgs a, int64_t batch, hipStream_t st) {
-  const size_t lds = lu_lds_bytes(a.n, NB);
+  const size_t lds = lu_lds_bytes(a.n, NB, NB == 32);  // 32-wide split panels keep only L11 in LDS
   if (lds > kLdsMax) return RNR_ERR_UNSUPPORTED_N;
   if (int e = set_lds(k_lu<PIVOT, NB, RPT, true>, lds)) return e;
   for (int k0 = 0; k0 < a.n; k0 += NB) {
@@ -128,6 +128,10 @@ int launch_lu_split(LuArgs a, int64_t batch, hipStream_t st) {
     if (k1 >= a.n) break;
     const int nchunk = (a.n - k1 + 63) / 64, nrg = (a.n - k1 + kLuTrailRows - 1) / kLuTrailRows;
     k_lu_trail<PIVOT, NB><<<dim3((unsigned)(batch * nchunk * nrg)), dim3(kLuTrailThreads), 0, st>>>(a, nchunk, nrg);
+  }
+  if (!PIVOT && NB == 32) {  // the chart's tau, from the finished multipliers
+    const int ncb = (a.n + 31) / 32;
+    k_chart_tau<<<dim3((unsigned)(batch * ncb)), dim3(256), 0, st>>>(a.dst, a.sd, a.tau, a.n, ncb);
   }
   return hip_status();
 }
@@ -142,8 +146,10 @@ int launch_lu(bool pivot, const float* src, int64_t ss, float* dst, int64_t sd, 
   a.k0 = 0; a.X = xbuf;
   const int nb = lu_panel_nb(n);
   if (lu_split(batch, n) && xbuf) {
-    if (pivot) return nb == 32 ? launch_lu_split<true, 32, 2>(a, batch, st) : launch_lu_split<true, 16, 4>(a, batch, st);
-    return nb == 32 ? launch_lu_split<false, 32, 2>(a, batch, st) : launch_lu_split<false, 16, 4>(a, batch, st);
+    // 32-wide panels at every split size: the panel's rows go straight between HBM and registers,
+    // so its width is not bound by an n-row LDS copy (rank-32 trailing updates, half the passes)
+    if (pivot) return n <= 1024 ? launch_lu_split<true, 32, 2>(a, batch, st) : launch_lu_split<true, 32, 4>(a, batch, st);
+    return n <= 1024 ? launch_lu_split<false, 32, 2>(a, batch, st) : launch_lu_split<false, 32, 4>(a, batch, st);
   }
   // rows per thread: n <= kLuThreads * RPT
   if (pivot) {
