@@ -249,16 +249,24 @@ int launch_trsm(const float* M, int64_t sm, const int* mperm, const float* Wm, i
                 int64_t batch, int n, hipStream_t st) {
   TrsmArgs a;
   a.M = M; a.sm = sm; a.Wm = Wm; a.sw = sw; a.Dinv = Dinv; a.Q = Q; a.sq = sq; a.Q2 = Q2; a.sq2 = sq2;
-  a.perm = perm; a.mperm = mperm; a.n = n; a.nrb = (n + kTrsmRows - 1) / kTrsmRows;
+  // 64-row blocks when 128-row ones would give fewer than two workgroups per CU (small batches
+  // at large n): twice the workgroups for the same work
+  const bool half = batch * ((n + kTrsmRows - 1) / kTrsmRows) < 512;
+  const int rb = half ? 64 : kTrsmRows;
+  a.perm = perm; a.mperm = mperm; a.n = n; a.nrb = (n + rb - 1) / rb;
   const int64_t total = batch * a.nrb;
   if (total > INT32_MAX) return RNR_ERR_INVALID_ARG;
   a.total = (int)total;
   const bool vec4 = (n % 4 == 0) && (sq % 4 == 0) && (sm % 4 == 0) && aligned(Q, 16) && aligned(M, 16) &&
                     aligned(Wm, 16);
-  if (vec4)
-    k_trsm<true><<<dim3((unsigned)total), dim3(256), 0, st>>>(a);
-  else
-    k_trsm<false><<<dim3((unsigned)total), dim3(256), 0, st>>>(a);
+  const dim3 grid((unsigned)total), block(256);
+  if (half) {
+    if (vec4) k_trsm<true, 64><<<grid, block, 0, st>>>(a);
+    else k_trsm<false, 64><<<grid, block, 0, st>>>(a);
+  } else {
+    if (vec4) k_trsm<true, kTrsmRows><<<grid, block, 0, st>>>(a);
+    else k_trsm<false, kTrsmRows><<<grid, block, 0, st>>>(a);
+  }
   return hip_status();
 }
 

@@ -132,16 +132,21 @@ __global__ __launch_bounds__(256) void k_wblocks(WblkArgs a) {
   }
 }
 
-template <bool VEC4>
+// RB = 128: each wave owns 32 rows x 64 columns (two 32x32 accumulators); RB = 64 (small
+// batches at large n, twice the workgroups): 2 x 2 waves of 32 x 32.
+template <bool VEC4, int RB = kTrsmRows>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_trsm(TrsmArgs a) {
-  constexpr int RB = kTrsmRows, BK = 16, LDA = BK + 1;
+  constexpr int BK = 16, LDA = BK + 1;
+  constexpr int NP = RB / 64;    // A-chunk float4 slots per thread
+  constexpr int WN = 128 / RB;   // waves side by side across the 64 columns
+  constexpr int NACC = 2 / WN;   // 32x32 accumulators per wave
   __shared__ __attribute__((aligned(16))) float smA[2 * RB * LDA];  // A chunk: RB rows x BK
   __shared__ __attribute__((aligned(16))) float smB[2 * BK * 64];   // B chunk: BK x 64
   __shared__ __attribute__((aligned(16))) int prow[RB];
   __shared__ int mrow[RB];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int l32 = lane & 31, h = lane >> 5, wr = wid * 32;
+  const int l32 = lane & 31, h = lane >> 5, wr = (wid / WN) * 32, wc = (wid % WN) * 32 * NACC;
   const int pid = xcd_remap(blockIdx.x, a.total);
   const int b = pid / a.nrb, r0 = (pid - b * a.nrb) * RB, n = a.n;
   const float* M = a.M + b * a.sm;
@@ -165,17 +170,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   // set to zero.  Each thread's two A rows are fixed, so their offsets stay in registers.
   // The loads are used only by the LDS stores after the chunk's MFMAs, so nothing touches the
   // loaded registers before then: the diagonal chunk's masks are applied in lstore.
-  float ra[8], rb[4];
-  const int ia0 = tid >> 2, ia1 = 64 + (tid >> 2), ca = 4 * (tid & 3);
-  const int qo0 = prow[ia0] * n, qo1 = prow[ia1] * n;
-  const int mo0 = mrow[ia0] * n, mo1 = mrow[ia1] * n;
+  float ra[4 * NP], rb[4];
+  const int ca = 4 * (tid & 3);
+  int ia[NP], qo[NP], mo[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    ia[p] = (tid >> 2) + 64 * p;
+    qo[p] = prow[ia[p]] * n;
+    mo[p] = mrow[ia[p]] * n;
+  }
   const int kr = tid >> 4, cb = 4 * (tid & 15);
   auto gload = [&](int kc, int c0) {
     const int k = kc + ca;
     if (kc < c0) {  // Q (this workgroup's earlier output) against -W
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const float* src = Q + (p ? qo1 : qo0) + k;  // k + 3 < c0 <= n
+      for (int p = 0; p < NP; ++p) {
+        const float* src = Q + qo[p] + k;  // k + 3 < c0 <= n
         float4 v;
         if (VEC4) {
           v = *reinterpret_cast<const float4*>(src);
@@ -196,8 +206,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
       rb[0] = v.x; rb[1] = v.y; rb[2] = v.z; rb[3] = v.w;
     } else {  // the diagonal chunk: M (or the unit-lower view of L) against Dinv_c
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const float* mr = M + (p ? mo1 : mo0);
+      for (int p = 0; p < NP; ++p) {
+        const float* mr = M + mo[p];
         float4 v;
         if (VEC4) {
           v = *reinterpret_cast<const float4*>(mr + min(k, n - 4));
@@ -216,8 +226,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     if (kc >= c0) {  // uniform: the diagonal chunk
       if (a.mperm) {  // L[row][k]: stored below the diagonal, 1 on it, 0 above
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          int d = r0 + (p ? ia1 : ia0) - (kc + ca);  // row - k
+        for (int p = 0; p < NP; ++p) {
+          int d = r0 + ia[p] - (kc + ca);  // row - k
           asm volatile("" : "+v"(d));  // keeps the selects here instead of hoisted out of the loops
 #pragma unroll
           for (int q = 0; q < 4; ++q) ra[4 * p + q] = (q < d) ? ra[4 * p + q] : (q == d ? 1.f : 0.f);
@@ -226,18 +236,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
       if (kc + kr >= n) rb[0] = rb[1] = rb[2] = rb[3] = 0.f;  // K rows past n
     }
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int idx = tid + 256 * p;
-      const int i = idx >> 2, ca = 4 * (idx & 3);
+    for (int p = 0; p < NP; ++p) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) As[i * LDA + ca + q] = ra[4 * p + q];
+      for (int q = 0; q < 4; ++q) As[ia[p] * LDA + ca + q] = ra[4 * p + q];
     }
     *reinterpret_cast<float4*>(&Bs[(tid >> 4) * 64 + 4 * (tid & 15)]) = make_float4(rb[0], rb[1], rb[2], rb[3]);
   };
 
   for (int c0 = 0; c0 < n; c0 += 64) {
     const int kend = min(c0 + 64, n);
-    f32x16 acc[2] = {zero16(), zero16()};
+    f32x16 acc[NACC];
+#pragma unroll
+    for (int j = 0; j < NACC; ++j) acc[j] = zero16();
     int buf = 0;
     gload(0, c0);
     lstore(0, 0, c0);
@@ -251,8 +261,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
       for (int kk = 0; kk < BK; kk += 2) {
         const int k = kk + h;
         const float av = As[(wr + l32) * LDA + k];
-        acc[0] = mfma(av, Bs[k * 64 + l32], acc[0]);
-        acc[1] = mfma(av, Bs[k * 64 + 32 + l32], acc[1]);
+#pragma unroll
+        for (int j = 0; j < NACC; ++j) acc[j] = mfma(av, Bs[k * 64 + wc + 32 * j + l32], acc[j]);
       }
       if (more) lstore(buf ^ 1, kc + BK, c0);
       __syncthreads();
@@ -271,8 +281,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
-          for (int nj = 0; nj < 2; ++nj) {
-            const int col = c0 + nj * 32 + (ln & 31);
+          for (int nj = 0; nj < NACC; ++nj) {
+            const int col = c0 + wc + nj * 32 + (ln & 31);
             if (!decltype(masked)::value || (r0 + lb + q < n && col < n)) dst[prr[q] * n + col] = acc[nj][4 * g + q];
           }
       }
