@@ -285,22 +285,19 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
             const uint64_t wbest = wave_max_key(best);
             if (best == wbest) {  // exactly one lane: keys are distinct
               atomicMax(kcur, (unsigned long long)wbest);
-              // the winning row by selects (a branch per row would be merged into a
-              // lane-dependent index into row[], which puts row[] on the stack)
+              // the winning row: one masked store block per row of the thread, only the winner's
+              // executing (the stored values pass through an empty asm so the blocks are not
+              // merged into a lane-dependent index into row[], which would put row[] on the stack)
 #pragma unroll
-              for (int c4 = C0; c4 < NB4; ++c4) {
-                float4 w = make_float4(row[0][4 * c4], row[0][4 * c4 + 1], row[0][4 * c4 + 2], row[0][4 * c4 + 3]);
+              for (int q = 0; q < RPT; ++q) {
+                if (RPT == 1 || bq == q) {
 #pragma unroll
-                for (int q = 1; q < RPT; ++q) {
-                  const bool t = bq == q;
-                  float4 o = make_float4(row[q][4 * c4], row[q][4 * c4 + 1], row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
-                  asm volatile("" : "+v"(o.x), "+v"(o.y), "+v"(o.z), "+v"(o.w));  // opaque: no indexed form
-                  w.x = t ? o.x : w.x;
-                  w.y = t ? o.y : w.y;
-                  w.z = t ? o.z : w.z;
-                  w.w = t ? o.w : w.w;
+                  for (int c4 = C0; c4 < NB4; ++c4) {
+                    float4 o = make_float4(row[q][4 * c4], row[q][4 * c4 + 1], row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
+                    if (RPT > 1) asm volatile("" : "+v"(o.x), "+v"(o.y), "+v"(o.z), "+v"(o.w));
+                    sb[wid * SLOT4 + 1 + c4] = o;
+                  }
                 }
-                sb[wid * SLOT4 + 1 + c4] = w;
               }
             }
           }
