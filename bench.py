@@ -44,7 +44,7 @@ def _events_ms(fn, reps: int, stream) -> float:
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_headline_256x512.md")
 # bench kernel label -> the kernel symbol in the rocprofv3 counter summary
 # rocprofv3 symbols of each reported kernel and their launches per step
-PROFILE_SYMBOL = {"k_trsm": [("rnr::k_trsm<true>", 2)], "k_chol": [("rnr::k_chol", 2)],
+PROFILE_SYMBOL = {"k_trsm": [("rnr::k_trsm<true, 128>", 2)], "k_chol": [("rnr::k_chol", 2)],
                   "k_lu<true> (LU)": [("rnr::k_lu<true, 64, 1, false>", 1)],
                   "k_lu<false> (chart)": [("rnr::k_lu<false, 64, 1, false>", 1)],
                   "k_tn_upper": [("rnr::k_tn_upper<128, false, false, true, 16, true>", 1),
