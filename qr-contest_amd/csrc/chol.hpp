@@ -453,9 +453,15 @@ __global__ __launch_bounds__(64) void k_chol_diag(CholSplitArgs a) {
   const int kb = min(kCholNb, n - k0);
   float* G = a.G + b * a.sg;
   float* Dv = a.Dinv + (int64_t)b * n * 64;
-  for (int idx = lane; idx < 64 * 64; idx += 64) {
-    const int i = idx >> 6, c = idx & 63;
-    D[i * 65 + c] = (i < kb && c < kb) ? G[(k0 + i) * n + k0 + c] : (i == c ? 1.f : 0.f);
+  {
+    // the block row by row, the lanes along each row: all 64 loads in flight together
+    // (addresses clamped past n, the identity written there)
+    const int cl = min(lane, kb - 1);
+    float v[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) v[i] = G[(k0 + min(i, kb - 1)) * n + k0 + cl];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) D[i * 65 + lane] = (i < kb && lane < kb) ? v[i] : (i == lane ? 1.f : 0.f);
   }
   wave_lds_order();
   const int fail = chol_diag_wave(D, XT, RI, SB, lane);
@@ -463,8 +469,9 @@ __global__ __launch_bounds__(64) void k_chol_diag(CholSplitArgs a) {
   wave_lds_order();
   chol_inverse_wave(XT, RI, D, XT, lane);
   wave_lds_order();
-  for (int idx = lane; idx < kb * 64; idx += 64) {
-    const int i = idx >> 6, c = idx & 63;
+#pragma unroll 16
+  for (int i = 0; i < kb; ++i) {
+    const int c = lane;
     if (c < kb && c >= i) G[(k0 + i) * n + k0 + c] = D[i * 65 + c];
     Dv[(k0 + i) * 64 + c] = (c < kb) ? XT[c * 65 + i] : 0.f;
   }
