@@ -488,17 +488,27 @@ __global__ __launch_bounds__(kCholSplitThreads) void k_chol_row(CholSplitArgs a)
   const int job = 4 * (int)(pid - b * a.njob) + wid;
   float* G = a.G + b * a.sg;
   const float* Dv = a.Dinv + b * n * 64;
-  for (int idx = tid; idx < 64 * 64; idx += kCholSplitThreads) {
-    const int i = idx >> 6, c = idx & 63;  // XT[c][i] = Dinv_kk[i][c]
-    XT[c * 65 + i] = Dv[(k0 + i) * 64 + c];
-  }
-  __syncthreads();
-  if (32 * job >= w) return;
+  // the job's block-row operand is loaded first (clamped for jobs past the end, which only
+  // stage Dinv), then Dinv_kk with all its loads in flight together
   const int colr = job * 32 + l32, col = k1 + colr;
   const int base = (k0 + h) * n + min(col, n - 1);  // columns past n: computed, not stored
   float bv[32];
 #pragma unroll
   for (int t = 0; t < 32; ++t) bv[t] = G[base + 2 * t * n];
+  constexpr int DPT = 64 * 64 / kCholSplitThreads;
+  float dv[DPT];
+#pragma unroll
+  for (int u = 0; u < DPT; ++u) {
+    const int idx = tid + kCholSplitThreads * u, i = idx >> 6, c = idx & 63;
+    dv[u] = Dv[(k0 + i) * 64 + c];
+  }
+#pragma unroll
+  for (int u = 0; u < DPT; ++u) {
+    const int idx = tid + kCholSplitThreads * u, i = idx >> 6, c = idx & 63;  // XT[c][i] = Dinv_kk[i][c]
+    XT[c * 65 + i] = dv[u];
+  }
+  __syncthreads();
+  if (32 * job >= w) return;
   f32x16 acc0 = zero16(), acc1 = zero16();
 #pragma unroll
   for (int t = 0; t < 32; ++t) {
@@ -540,7 +550,7 @@ __global__ __launch_bounds__(kCholSplitThreads) void k_chol_trail(CholSplitArgs 
         acc[mi][nj][r] = G[row * n + col];
       }
   const int ci0 = I * 64 + l32, cj0 = J * 64 + l32;  // reads past w reach unstored entries only
-#pragma unroll 8
+#pragma unroll
   for (int kk = 0; kk < kCholNb; kk += 2) {
     const float* gk = G + (k0 + kk + h) * n + k1;
     const float av[2] = {-gk[ci0], -gk[ci0 + 32]}, bv[2] = {gk[cj0], gk[cj0 + 32]};
