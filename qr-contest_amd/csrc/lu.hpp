@@ -654,8 +654,17 @@ __global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail(LuArgs a, int nchu
   const int c0 = k1 + 64 * (rem - rg * nchunk);
   const float* cur = ((k0 == 0) ? a.src + b * a.ss : a.dst + b * a.sd);
   float* dst = a.dst + b * a.sd;
-  for (int i = k0 + tid; i < n; i += kLuTrailThreads) pls[i] = PIVOT ? a.perm[b * n + i] : i;
-  for (int idx = tid; idx < NB * NB; idx += kLuTrailThreads) Xs[idx / NB][idx % NB] = a.X[b * NB * NB + idx];
+  // staging loops with compile-time trip counts, so their loads issue together
+#pragma unroll
+  for (int u = 0; u < RNR_MAX_N / kLuTrailThreads; ++u) {
+    const int i = k0 + tid + kLuTrailThreads * u;
+    if (i < n) pls[i] = PIVOT ? a.perm[b * n + i] : i;
+  }
+#pragma unroll
+  for (int u = 0; u < NB * NB / kLuTrailThreads; ++u) {
+    const int idx = tid + kLuTrailThreads * u;
+    Xs[idx / NB][idx % NB] = a.X[b * NB * NB + idx];
+  }
   __syncthreads();
 
   // -U12 chunk: (NB/16) x 4 blocks of 16x16
@@ -680,7 +689,9 @@ __global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail(LuArgs a, int nchu
   const int ntr = min((n - k1 + 31) >> 5, (rg + 1) * (kLuTrailRows / 32));
   for (int tr = rg * (kLuTrailRows / 32) + wid; tr < ntr; tr += NW) {
     const int r0 = k1 + tr * 32;
-    // L21 rows r0 .. r0 + 31 (columns k0 .. k1) into this wave's tile
+    // L21 rows r0 .. r0 + 31 (columns k0 .. k1) into this wave's tile (unrolled: the loads
+    // issue together)
+#pragma unroll
     for (int idx = lane; idx < 32 * NB; idx += 64) {  // rows past n clamped: never stored
       const int rr = idx / NB, k = idx - rr * NB, rw = min(r0 + rr, n - 1);
       Ls[wid][rr][k] = dst[pls[rw] * n + k0 + k];
