@@ -42,34 +42,60 @@ def _events_ms(fn, reps: int, stream) -> float:
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_headline_256x512.md")
-# bench kernel label -> the kernel symbol in the rocprofv3 counter summary
-# rocprofv3 symbols of each reported kernel and their launches per step
-PROFILE_SYMBOL = {"k_trsm": [("rnr::k_trsm<true, 128>", 2)], "k_chol": [("rnr::k_chol", 2)],
-                  "k_lu<true> (LU)": [("rnr::k_lu<true, 64, 1, false>", 1)],
-                  "k_lu<false> (chart)": [("rnr::k_lu<false, 64, 1, false>", 1)],
-                  "k_tn_upper": [("rnr::k_tn_upper<128, false, false, true, 16, true>", 1),
-                                 ("rnr::k_tn_upper<128, false, false, true, 16, false>", 1),
-                                 ("rnr::k_tn_upper<128, true, true, true, 16, false>", 1)]}
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` (mean over its launches in one step) from the committed
-    rocprofv3 FETCH/WRITE summary (headline workload only), or None."""
-    syms = PROFILE_SYMBOL.get(kernel)
-    if not syms:
-        return None
-    per = {}
+def stage_symbols(batch: int, n: int) -> dict:
+    """The rocprofv3 kernel symbol behind each stage of rnr_qr_f32 (the stages its timed twin
+    brackets), following the library's dispatch rules (csrc/rnrqr.hip: lu_split, launch_lu,
+    launch_tn, launch_chol, launch_trsm).  Split-form stages span several symbols ("a + b")."""
+    if n <= 64:
+        np_ = 16 if n <= 16 else (32 if n <= 32 else 64)
+        return {"path": f"rnr::k_small<{np_}>"}
+    split = n > 512 and batch < 128
+    vec4 = n % 4 == 0
+    tf = lambda b: "true" if b else "false"  # noqa: E731
+    if split:
+        rpt = 2 if n <= 1024 else 4
+        lu = f"rnr::k_lu<true, 32, {rpt}, true> + rnr::k_lu_trail<true, 32>"
+        chart = f"rnr::k_lu<false, 32, {rpt}, true> + rnr::k_lu_trail<false, 32> + rnr::k_chart_tau"
+        chol = "rnr::k_chol_jitter + rnr::k_chol_diag + rnr::k_chol_row + rnr::k_chol_trail"
+    else:
+        nb, rpt = (64, 1) if n <= 512 else ((32, 2) if n <= 1024 else (16, 4))
+        lu = f"rnr::k_lu<true, {nb}, {rpt}, false>"
+        chart = f"rnr::k_lu<false, {nb}, {rpt}, false>"
+        chol = "rnr::k_chol"
+    big = n > 256
+    bm = 128 if big else 64
+
+    def tn(closure: bool, lperm: bool) -> str:
+        if closure:
+            bk, lv = (16 if (big and vec4) else 32), False
+        elif big and vec4:
+            bk, lv = 16, lperm
+        else:
+            bk, lv = 32, True
+        return f"rnr::k_tn_upper<{bm}, {tf(closure)}, {tf(closure)}, {tf(vec4)}, {bk}, {tf(lv)}>"
+
+    rb = 64 if batch * ((n + 127) // 128) < 512 else 128
+    trsm = f"rnr::k_trsm<{tf(vec4)}, {rb}>"
+    return {"lu": lu, "gram_L": tn(False, True), "chol_1": chol, "wblk_1": "rnr::k_wblocks", "trsm_1": trsm,
+            "gram_Q1": tn(False, False), "chol_2": chol, "wblk_2": "rnr::k_wblocks", "trsm_2": trsm,
+            "chart": chart, "closure": tn(True, False)}
+
+
+def measured_traffic(symbol: str):
+    """HBM bytes per launch of the kernel `symbol` from the committed rocprofv3 FETCH / WRITE
+    summary (headline workload only), or None."""
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
                 if line.startswith("traffic "):
                     name, val = line[len("traffic "):].rsplit(" ", 1)
-                    per[name] = int(val)
+                    if name == symbol:
+                        return int(val)
     except OSError:
-        return None
-    if not all(s in per for s, _ in syms):
-        return None
-    return int(sum(per[s] * c for s, c in syms) / sum(c for _, c in syms))
+        pass
+    return None
 
 
 def _cpu_name() -> str:
@@ -87,10 +113,15 @@ def cpu_baseline(A_cpu: torch.Tensor, classes: int, budget_s: float = 10.0):
     """The oracle (torch-CPU restatement of the reference, fp32) on a bounded sample."""
     from oracle import rnr as orc
 
-    # torch's own intra-op thread count (OMP_NUM_THREADS where set).  It is deliberately not
-    # changed: calling torch.set_num_threads at all makes this image's MKL batched sgetrf fail
-    # (SLASWP parameter error, then a hang) on these inputs.
+    # torch's own intra-op thread count (OMP_NUM_THREADS where set) is what the timed code
+    # uses.  It is deliberately not changed: calling torch.set_num_threads at all makes this
+    # image's MKL batched sgetrf fail (SLASWP parameter error, then a hang) on these inputs.
+    # The cores the process may run on are reported beside it.
     cores = torch.get_num_threads()
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
     sample = A_cpu[: max(1, classes)].contiguous()
     orc.custom_kernel(sample[:1])  # warm-up
     t0 = time.perf_counter()
@@ -110,6 +141,9 @@ def cpu_baseline(A_cpu: torch.Tensor, classes: int, budget_s: float = 10.0):
         "value": sample.shape[0] / dt,
         "unit": "matrices/s",
         "cores": cores,
+        "affinity_cores": affinity,
+        "threads_note": "cores = torch intra-op threads actually used (OMP_NUM_THREADS); affinity_cores = "
+                        "len(os.sched_getaffinity(0))",
         "kind": "port",
         "sample": f"first {sample.shape[0]} matrices of the same batch (every class), "
                   f"{reps} repetitions in {dt * reps:.1f} s; CPU: {_cpu_name()}",
@@ -191,9 +225,12 @@ def main() -> None:
         torch.cuda.synchronize()
         chk_ms = (time.perf_counter() - t_chk) * 1e3
         info_ok = int(plan.info.abs().sum().item()) == 0
+        finite = bool(torch.isfinite(plan.H).all()) and bool(torch.isfinite(plan.tau).all())
+        tau_ok = plan.tau.min().item() >= 1.0 - 16 * 1.1920928955078125e-07 and plan.tau.max().item() <= 2.0
         gates = {"factor_max": fr, "factor_gate": ft, "ortho_max": og, "ortho_gate": ot,
                  "percol_max": ratio, "checked": cfg.batch, "checker": "rnr_check_f64 (GPU, float64)",
-                 "checker_ms": chk_ms, "pass": bool(ok.all()) and bool(ok_col.all()) and info_ok}
+                 "checker_ms": chk_ms, "finite": finite, "tau_in_range": tau_ok,
+                 "pass": bool(ok.all()) and bool(ok_col.all()) and info_ok and finite and tau_ok}
 
     # the steps either side of the path: the input generators and the Q consumers
     aux = None
@@ -246,18 +283,28 @@ def main() -> None:
         for i, k in enumerate(native.QR_STAGES):
             stage_ms[k] += evs[i].elapsed_time(evs[i + 1]) / reps
 
-    # algorithmic flops per matrix of each launch (minimal counts, not what the kernel executes)
+    # algorithmic flops per matrix of each stage (minimal counts, not what the kernels execute;
+    # the W blocks are this build's restructuring of the solve and carry none of their own)
     n3 = float(cfg.n) ** 3
-    flops = {"lu": 2 / 3 * n3, "gram_L": n3 / 3, "chol_1": n3 / 3, "trsm_1": n3, "gram_Q1": n3,
-             "chol_2": n3 / 3, "trsm_2": n3, "chart": 2 / 3 * n3, "closure": n3}
-    kernels = {"k_lu<true> (LU)": ["lu"], "k_lu<false> (chart)": ["chart"], "k_chol": ["chol_1", "chol_2"],
-               "k_trsm": ["trsm_1", "trsm_2"], "k_tn_upper": ["gram_L", "gram_Q1", "closure"]}
+    flops = {"lu": 2 / 3 * n3, "gram_L": n3 / 3, "chol_1": n3 / 3, "wblk_1": 0.0, "trsm_1": n3, "gram_Q1": n3,
+             "chol_2": n3 / 3, "wblk_2": 0.0, "trsm_2": n3, "chart": 2 / 3 * n3, "closure": n3}
+    if cfg.n <= 64:  # one fused launch: the whole path's algorithmic flops
+        flops = {"path": sum(flops.values())}
+        stage_ms = {"path": sum(stage_ms.values())}
+    # stages grouped by the kernel symbol rocprofv3 reports for them (one row per symbol)
+    syms = stage_symbols(cfg.batch, cfg.n)
     per_kernel = {}
-    for name, ks in kernels.items():
-        t = sum(stage_ms[k] for k in ks)
-        f = sum(flops[k] for k in ks) * cfg.batch
-        per_kernel[name] = {"ms_per_step": t, "launches": len(ks), "avg_launch_us": 1e3 * t / len(ks),
-                            "tflops": f / (t / 1e3) / 1e12}
+    for stage, sym in syms.items():
+        k = per_kernel.setdefault(sym, {"stages": [], "ms_per_step": 0.0, "launches": 0, "gflop": 0.0})
+        k["stages"].append(stage)
+        k["ms_per_step"] += stage_ms[stage]
+        k["launches"] += 1
+        k["gflop"] += flops[stage] * cfg.batch / 1e9
+    for sym, k in per_kernel.items():
+        k["avg_launch_us"] = 1e3 * k["ms_per_step"] / k["launches"]
+        k["tflops"] = k["gflop"] / k["ms_per_step"] if k["ms_per_step"] > 0 else 0.0
+        k["frac_fp32_mfma"] = k["tflops"] / PEAK_FP32_MFMA_TFLOPS
+        k["share_of_step"] = k["ms_per_step"] / sum(stage_ms.values())
     dom = max(per_kernel, key=lambda k: per_kernel[k]["ms_per_step"])
     dom_tflops = per_kernel[dom]["tflops"]
 
@@ -298,6 +345,9 @@ def main() -> None:
             "traffic": measured_traffic(dom) if args.config == 4 else None,
             "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if args.config == 4 else None,
             "kernel": dom,
+            "basis": "the kernel symbol with the largest share of the step (hipEvent time per stage, "
+                     "stages grouped by symbol); achieved = its algorithmic flops per launch / its "
+                     "average launch time",
         },
         "path": {
             "nominal_tflops": nominal_tflops,

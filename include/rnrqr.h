@@ -74,13 +74,15 @@ int rnr_qr_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride,
                void* ws, size_t ws_bytes, rnr_stream_t stream);
 
 /* Same as rnr_qr_f32, and records events[i] (hipEvent_t handles created by the caller) on
- * the stream before launch i of the sequence and events[9] after the last, for per-kernel
- * timing of the live path: 0 LU, 1 Gram(L), 2 Cholesky (with the solve's off-diagonal
- * operand), 3 solve L R^-1, 4 Gram(Q1), 5 Cholesky (same), 6 solve Q1 R^-1 with the row
- * gather, 7 chart, 8 closure.  For n <= 64 the
- * path is one launch: events[0] before it and events[1..9] after it.  Stands in for the
- * reference's event timers around its stages (common/bench.py:12-21). */
-#define RNR_QR_TIMED_EVENTS 10
+ * the stream before stage i of the sequence and events[11] after the last, for per-kernel
+ * timing of the live path: 0 LU, 1 Gram(L), 2 Cholesky, 3 the solve's off-diagonal operand
+ * (W blocks), 4 solve L R^-1, 5 Gram(Q1), 6 Cholesky, 7 W blocks, 8 solve Q1 R^-1 with the
+ * row gather, 9 chart, 10 closure.  A stage is one launch, except in the split form (n > 512
+ * with fewer than 128 matrices), where the LU, Cholesky and chart stages are one launch per
+ * panel or block.  For n <= 64 the path is one launch: events[0] before it and
+ * events[1..11] after it.  Stands in for the reference's event timers around its stages
+ * (common/bench.py:12-21). */
+#define RNR_QR_TIMED_EVENTS 12
 int rnr_qr_f32_timed(const float* A, int64_t batch, int64_t n, int64_t batch_stride,
                      float* H, float* tau, int32_t* info, void* ws, size_t ws_bytes,
                      rnr_stream_t stream, void* const* events, int n_events);

@@ -20,9 +20,10 @@ RNR_ERR_WORKSPACE = 3
 RNR_ERR_HIP = 4
 RNR_ERR_MISALIGNED = 5
 RNR_MAX_N = 2048
-RNR_QR_TIMED_EVENTS = 10
-# the launches of rnr_qr_f32 in order (what rnr_qr_f32_timed's events bracket)
-QR_STAGES = ("lu", "gram_L", "chol_1", "trsm_1", "gram_Q1", "chol_2", "trsm_2", "chart", "closure")
+RNR_QR_TIMED_EVENTS = 12
+# the stages of rnr_qr_f32 in order (what rnr_qr_f32_timed's events bracket)
+QR_STAGES = ("lu", "gram_L", "chol_1", "wblk_1", "trsm_1", "gram_Q1", "chol_2", "wblk_2", "trsm_2", "chart",
+             "closure")
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p

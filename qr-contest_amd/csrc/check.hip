@@ -106,6 +106,10 @@ struct RedArgs {
   int n, nt;
 };
 
+// Maximum that keeps NaN (fmax drops it): a NaN residual must fail the gates, as it does in
+// the reference checker, whose comparisons with the gate are false for NaN.
+__device__ __forceinline__ double max_nan(double x, double y) { return (x > y || x != x) ? x : y; }
+
 __global__ __launch_bounds__(256) void k_chk_red(RedArgs a) {
   __shared__ double r_e[256], r_a[256], r_o[256], r_c[256];
   const int b = blockIdx.x, tid = threadIdx.x, n = a.n;
@@ -118,19 +122,19 @@ __global__ __launch_bounds__(256) void k_chk_red(RedArgs a) {
       o += a.po[((int64_t)b * a.nt + t) * n + j];
     }
     for (int i = 0; i < n; ++i) s += fabs((double)a.A[b * a.sa + (int64_t)i * n + j]);
-    me = fmax(me, e);
-    ma = fmax(ma, s);
-    mo = fmax(mo, o);
-    mc = fmax(mc, e / (ftol * fmax(s, 1e-300)));
+    me = max_nan(me, e);
+    ma = max_nan(ma, s);
+    mo = max_nan(mo, o);
+    mc = max_nan(mc, e / (ftol * fmax(s, 1e-300)));
   }
   r_e[tid] = me; r_a[tid] = ma; r_o[tid] = mo; r_c[tid] = mc;
   __syncthreads();
   for (int off = 128; off > 0; off >>= 1) {
     if (tid < off) {
-      r_e[tid] = fmax(r_e[tid], r_e[tid + off]);
-      r_a[tid] = fmax(r_a[tid], r_a[tid + off]);
-      r_o[tid] = fmax(r_o[tid], r_o[tid + off]);
-      r_c[tid] = fmax(r_c[tid], r_c[tid + off]);
+      r_e[tid] = max_nan(r_e[tid], r_e[tid + off]);
+      r_a[tid] = max_nan(r_a[tid], r_a[tid + off]);
+      r_o[tid] = max_nan(r_o[tid], r_o[tid + off]);
+      r_c[tid] = max_nan(r_c[tid], r_c[tid + off]);
     }
     __syncthreads();
   }

@@ -10,8 +10,8 @@
 //     (n <= 576), otherwise it is read back from G;
 //   * the trailing update G_>,> -= R_k,>^T R_k,> (upper 64x64 tiles, MFMA) is split: the
 //     first diagonal tile -- the next diagonal block -- is updated into LDS by quadrants on
-//     waves 0, 1 and 3 (three SIMDs; its lower-left quadrant is never read), then wave 0
-//     factors it (one symmetric row per lane in registers, the scaled pivot row broadcast
+//     waves 0, 1 and 3 (three SIMDs; its lower-left quadrant is never read), then, after a
+//     workgroup barrier, wave 0 factors it (one symmetric row per lane in registers, the scaled pivot row broadcast
 //     through LDS inside the wave, no barriers) and forms its inverse blocked by 32, while
 //     waves 1..7 update the other tiles.  The sequential diagonal work thus runs under the
 //     trailing update.
@@ -177,7 +177,6 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
   float* SB = RI + 64;             // [64] scaled pivot row broadcast (wave 0)
   float* red = SB + 64;            // [16]
   int* ffail = reinterpret_cast<int*>(red + 16);
-  int* dcnt = ffail + 1;           // diagonal-tile quadrants written by waves 1 and 3, so far
   float* S = red + 32;             // block row [64][n-64] when strip_lds
 
   const int n = a.n, b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -193,10 +192,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
   if (lane == 0) red[wid] = part;
-  if (tid == 0) {
-    *ffail = INT_MAX;
-    *dcnt = 0;
-  }
+  if (tid == 0) *ffail = INT_MAX;
   __syncthreads();
   float tot = 0.f;
 #pragma unroll
@@ -297,13 +293,13 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
           D[i * 65 + c] = (i < kbn && c < kbn) ? q[r] : (i == c ? 1.f : 0.f);
         }
       };
-      // the next diagonal tile's quadrants (0,1) and (1,1) run on waves 1 and 3, other SIMDs
-      // than wave 0's, before their own tiles; its quadrant (1,0) lies below the diagonal,
-      // which the factor never reads
-      if (!first && (wid == 1 || wid == 3)) {
-        diag_quadrant(wid == 3 ? 1 : 0, 1);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        if (lane == 0) atomicAdd(dcnt, 1);
+      // the next diagonal tile is updated by quadrants on three SIMDs at once -- (0,0) on wave
+      // 0, (0,1) and (1,1) on waves 1 and 3; its quadrant (1,0) lies below the diagonal, which
+      // the factor never reads -- and one barrier later wave 0 factors it while the other
+      // waves take the remaining tiles
+      if (!first) {
+        if (wid == 0 || wid == 1 || wid == 3) diag_quadrant(wid == 3 ? 1 : 0, wid == 0 ? 0 : 1);
+        __syncthreads();
       }
       auto diag_factor = [&]() {
         wave_lds_order();
@@ -313,22 +309,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
         chol_inverse_wave(RT, RI, D, XT, lane);
       };
       for (int pr = t0; pr < npairs; pr += tstep) {
-        if (pr == 0 && !first) {
-          // wave 0: quadrant (0,0), then wait for the other two (a bounded wait: past the
-          // limit the block is reported as failed instead of hanging)
-          diag_quadrant(0, 0);
-          const int target = 2 * (k0 / kCholNb + 1);
-          for (int spin = 0;; ++spin) {
-            const int got = __builtin_amdgcn_readfirstlane(
-                __hip_atomic_load(dcnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-            if (got >= target) break;
-            if (spin > (1 << 20)) {
-              if (lane == 0 && *ffail == INT_MAX) *ffail = k1 + 1;
-              break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-          }
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        if (pr == 0 && !first) {  // wave 0: the next diagonal tile, complete in D since the barrier
           diag_factor();
           continue;
         }

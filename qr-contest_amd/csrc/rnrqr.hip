@@ -5,6 +5,8 @@
 //   2. k_tn_upper        G = L^T L, upper tiles, zero rows of L skipped         (:73)
 //   3. k_chol            G -> R_a (upper, jittered), Dinv, info                 (:74-76)
 //      k_wblocks         W = off-diagonal blocks of R_a times Dinv -> Qb (the solve's operand)
+//                        (n > 512 with fewer than 128 matrices: k_chol_jitter, then per
+//                        64-column block k_chol_diag / k_chol_row / k_chol_trail instead of k_chol)
 //   4. k_trsm            Q1 = L R_a^-1 -> L buffer                              (:77)
 //   5. k_tn_upper        G = Q1^T Q1                                            (:73)
 //   6. k_chol            G -> R_b, Dinv, info                                   (:74-76)
@@ -213,8 +215,8 @@ int launch_wblocks(const float* R, int64_t sr, const float* Dinv, float* Wm, int
   return hip_status();
 }
 
-int launch_chol(float* G, int64_t sg, float* Dinv, float* Wm, int* info, int64_t batch, int n,
-                bool keep_info, hipStream_t st) {
+int launch_chol(float* G, int64_t sg, float* Dinv, int* info, int64_t batch, int n, bool keep_info,
+                hipStream_t st) {
   CholArgs a;
   a.G = G; a.sg = sg; a.Dinv = Dinv; a.info = info; a.n = n;
   a.keep_info = keep_info ? 1 : 0;
@@ -240,8 +242,7 @@ int launch_chol(float* G, int64_t sg, float* Dinv, float* Wm, int* info, int64_t
     if (int e = set_lds(k_chol, lds)) return e;
     k_chol<<<dim3((unsigned)batch), dim3(kCholThreads), lds, st>>>(a);
   }
-  if (int e = hip_status()) return e;
-  return launch_wblocks(G, sg, Dinv, Wm, batch, n, st);
+  return hip_status();
 }
 
 int launch_trsm(const float* M, int64_t sm, const int* mperm, const float* Wm, int64_t sw,
@@ -308,7 +309,9 @@ int cholqr_pass(const float* M, int64_t sm, const int* lperm, float* G, float* D
   if (int e = launch_tn(false, M, sm, M, sm, G, nn, nullptr, lperm, batch, n, lperm != nullptr, st))
     return e;
   if (int e = mk.mark(st)) return e;
-  if (int e = launch_chol(G, nn, Dinv, Wm, info, batch, n, keep_info, st)) return e;
+  if (int e = launch_chol(G, nn, Dinv, info, batch, n, keep_info, st)) return e;
+  if (int e = mk.mark(st)) return e;
+  if (int e = launch_wblocks(G, nn, Dinv, Wm, batch, n, st)) return e;
   if (int e = mk.mark(st)) return e;
   return launch_trsm(M, sm, lperm, Wm, nn, Dinv, Q, nn, Q2, nn, perm, batch, n, st);
 }

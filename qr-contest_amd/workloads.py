@@ -26,7 +26,7 @@ from dataclasses import dataclass
 import torch
 
 __all__ = ["CONFIGS", "Config", "make_batch", "haar", "with_singular_values",
-           "HEADLINE_CLASSES", "headline_class_batch"]
+           "HEADLINE_CLASSES", "headline_class_batch", "STRESS_CASES", "stress_batch"]
 
 
 @dataclass(frozen=True)
@@ -155,3 +155,74 @@ def well_conditioned(b: int, n: int, seed: int = 0, device="cpu", lo: float = -2
     gen.manual_seed(seed)
     A = with_singular_values(b, torch.logspace(0, lo, n, dtype=torch.float64), gen, device)
     return A.to(dtype).contiguous()
+
+
+# ----------------------------------------------------------------------------- stress battery
+# The reference's nine generator cases (common/oracle.py:43-146, dispatched by make_batch at
+# :126-146), which its validation scripts run over n in {176, ..., 4096} and seeds 0..7
+# (householder/_validate_v3.py:8-28, householder/tf32_seedvar_derisk.py:28-40).  Built the way
+# the reference builds them -- float32 throughout, orthogonal factors as the plain Q of a
+# Gaussian matrix -- on any device (the tests run them on the GPU, where the reference's
+# generators run too).
+STRESS_CASES = ("dense", "mixed", "rankdef", "nearrank", "clustered", "banded", "rowscaled",
+                "nearcollinear", "uppertri")
+
+
+def _stress_gauss(b, n, gen, device):
+    return torch.randn(b, n, n, dtype=torch.float32, generator=gen, device=device)
+
+
+def _stress_sv(b, n, sigma, gen, device):
+    """U diag(sigma) V^T with U, V the Q factors of Gaussian matrices (oracle.py:53-57)."""
+    U = torch.linalg.qr(_stress_gauss(b, n, gen, device))[0]
+    V = torch.linalg.qr(_stress_gauss(b, n, gen, device))[0]
+    return (U * sigma.view(1, 1, n)) @ V.mT.contiguous()
+
+
+def _stress_head(n, device, tail):
+    """n/2 singular values logspace(0, -1), the rest `tail` (oracle.py:60-73)."""
+    r = n // 2
+    s = torch.full((n,), float(tail), dtype=torch.float32, device=device)
+    s[:r] = torch.logspace(0, -1, r, device=device)
+    return s
+
+
+def _stress_one(case, b, n, cond, gen, device):
+    if case == "dense":  # columns scaled by logspace(0, -cond, n) (oracle.py:48-51)
+        return _stress_gauss(b, n, gen, device) * torch.logspace(0, -float(cond), n, device=device).view(1, 1, n)
+    if case == "rankdef":
+        return _stress_sv(b, n, _stress_head(n, device, 0.0), gen, device)
+    if case == "nearrank":
+        return _stress_sv(b, n, _stress_head(n, device, 1e-8), gen, device)
+    if case == "clustered":  # two clusters, 1 and 1e-6 (oracle.py:76-79)
+        s = torch.ones(n, device=device)
+        s[n // 2:] = 1e-6
+        return _stress_sv(b, n, s, gen, device)
+    if case == "mixed":  # dense, every fourth matrix a stress case in turn (oracle.py:82-90)
+        A = _stress_one("dense", b, n, cond, gen, device)
+        stress = ("rankdef", "nearrank", "clustered")
+        for i in range(3, b, 4):
+            A[i] = _stress_one(stress[(i // 4) % 3], 1, n, cond, gen, device)[0]
+        return A
+    if case == "banded":  # zero outside |i - j| <= n / 8 (oracle.py:98-106)
+        bw = max(1, n // 8)
+        i = torch.arange(n, device=device)
+        band = (i.view(n, 1) - i.view(1, n)).abs() <= bw
+        return _stress_gauss(b, n, gen, device) * band.view(1, n, n)
+    if case == "rowscaled":  # rows scaled by logspace(0, -cond, n) (oracle.py:109-113)
+        return _stress_gauss(b, n, gen, device) * torch.logspace(0, -float(cond), n, device=device).view(1, n, 1)
+    if case == "nearcollinear":  # column 1 = column 0 + 1e-7 noise (oracle.py:116-121)
+        A = _stress_gauss(b, n, gen, device)
+        noise = torch.randn(b, n, dtype=torch.float32, generator=gen, device=device)
+        A[:, :, 1] = A[:, :, 0] + 1e-7 * noise
+        return A
+    if case == "uppertri":
+        return torch.triu(_stress_gauss(b, n, gen, device))
+    raise ValueError(f"unknown stress case {case!r}")
+
+
+def stress_batch(case: str, b: int, n: int, cond: float = 2.0, seed: int = 0, device="cpu") -> torch.Tensor:
+    """b float32 matrices of one of the reference's nine stress cases (STRESS_CASES)."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(int(seed))
+    return _stress_one(case, int(b), int(n), cond, gen, device).contiguous()

@@ -29,6 +29,10 @@ CASES = [
     ("randn_1x96", 1, 96, 103, "randn"),
     ("wellcond_2x64", 2, 64, 104, "wellcond"),
     ("uppertri_2x24", 2, 24, 105, "uppertri"),
+    # benchmark-size cases: the blocked path (64-wide panels, 64-column Cholesky blocks,
+    # 128-row solve blocks at 512; the 64-wide tiles of the mid sizes at 128)
+    ("wellcond_2x128", 2, 128, 106, "wellcond"),
+    ("wellcond_2x512", 2, 512, 107, "wellcond"),
 ]
 
 

@@ -73,26 +73,68 @@ def test_gpu_checker_exact_factorization_passes_tightly(chk):
     assert f.max().item() < 1e-5 and o.max().item() < 1e-5
 
 
+def test_gpu_checker_fails_nan(chk, rnr, wl):
+    """A NaN in R, in a reflector tail or in tau fails both gates, as in the reference checker
+    (whose `<` comparisons are False for NaN, common/oracle.py:166-168) and its CPU
+    restatement; the untouched matrices still pass."""
+    print("[case] checker NaN planting", flush=True)
+    A = wl.make_batch(4, batch=4, n=96, seed=9)
+    H, tau = rnr.custom_kernel(A.to(DEV))
+    H, tau = H.clone(), tau.clone()
+    H[0, 2, 5] = float("nan")
+    H[1, 9, 3] = float("nan")
+    tau[2, 4] = float("nan")
+    Ad = A.to(DEV)
+    _, _, _, _, ok = chk.check(Ad, H, tau)
+    _, _, okc = chk.check_percol(Ad, H, tau)
+    f, o, r = chk.gate_values(Ad, H, tau)
+    torch.cuda.synchronize()
+    assert ok.cpu().tolist() == [False, False, False, True], (f, o)
+    assert okc.cpu().tolist() == [False, False, False, True], (r, o)
+    _, _, _, _, okcpu = checker.check(A, H.cpu(), tau.cpu())
+    assert okcpu.tolist() == ok.cpu().tolist()
+
+
+def _full_batch_gates(chk, A, H, tau, label, margin=100.0):
+    assert bool(torch.isfinite(H).all()) and bool(torch.isfinite(tau).all()), label
+    assert tau.min().item() >= 1.0 - 16 * checker.EPS32 and tau.max().item() <= 2.0, label
+    fac, orth, ft, ot, ok = chk.check(A, H, tau)
+    ratio, _, okc = chk.check_percol(A, H, tau)
+    torch.cuda.synchronize()
+    print(f"{label}: factor {fac:.3e} (gate {ft:.3e}) ortho {orth:.3e} (gate {ot:.3e}) percol {ratio:.3e}")
+    assert bool(ok.all()) and bool(okc.all()), label
+    assert fac < ft / margin and orth < ot / margin, label  # the reference's own margins are ~1e5
+
+
 def test_full_headline_batch_passes_the_gates_on_gpu(chk, rnr, wl):
     """Configuration 4 at full size (256 x 512, six classes): every matrix within both gates and
     the per-column gate -- checked in float64 on the GPU."""
     print("[case] config 4 full batch gates on GPU", flush=True)
     A = wl.make_batch(4).to(DEV)
     H, tau = rnr.custom_kernel(A)
-    fac, orth, ft, ot, ok = chk.check(A, H, tau)
-    ratio, _, okc = chk.check_percol(A, H, tau)
-    torch.cuda.synchronize()
-    print(f"factor {fac:.3e} (gate {ft:.3e}) ortho {orth:.3e} (gate {ot:.3e}) percol {ratio:.3e}")
-    assert bool(ok.all()) and bool(okc.all())
-    assert fac < ft / 100 and orth < ot / 100  # the reference's own margins are ~1e5
+    _full_batch_gates(chk, A, H, tau, "config 4")
 
 
 def test_full_large_n_batch_passes_the_gates_on_gpu(chk, rnr, wl):
-    """Configuration 5 at full size (16 x 2048)."""
+    """Configuration 5 at full size (16 x 2048): the split form (one launch per panel)."""
     print("[case] config 5 full batch gates on GPU", flush=True)
     A = wl.make_batch(5).to(DEV)
     H, tau = rnr.custom_kernel(A)
-    fac, orth, ft, ot, ok = chk.check(A, H, tau)
-    torch.cuda.synchronize()
-    print(f"factor {fac:.3e} (gate {ft:.3e}) ortho {orth:.3e} (gate {ot:.3e})")
-    assert bool(ok.all())
+    _full_batch_gates(chk, A, H, tau, "config 5")
+
+
+def test_full_mid_batch_passes_the_gates_on_gpu(chk, rnr, wl):
+    """Configuration 3 at full size (1024 x 128, sigma in [1e-6, 1]): the 128-row solve blocks
+    that only a batch this large selects."""
+    print("[case] config 3 full batch gates on GPU", flush=True)
+    A = wl.make_batch(3).to(DEV)
+    H, tau = rnr.custom_kernel(A)
+    _full_batch_gates(chk, A, H, tau, "config 3")
+
+
+def test_full_small_n_batch_passes_the_gates_on_gpu(chk, rnr, wl):
+    """Configuration 2 at full size (4096 x 32): every matrix through the GPU checker."""
+    print("[case] config 2 full batch gates on GPU", flush=True)
+    A = wl.make_batch(2).to(DEV)
+    H, tau = rnr.custom_kernel(A)
+    _full_batch_gates(chk, A, H, tau, "config 2")

@@ -76,6 +76,90 @@ def _elementwise(A, H, tau):
     return e_hip, e_ref, d_ro
 
 
+def _first_sign_change(Hx, Hy):
+    """Per matrix, the first k where diag(Hx) and diag(Hy) differ in sign (n where none).
+
+    The diagonal of H is s_k R_kk, so a difference there is a different sign-rule choice at
+    column k of the chart.  Everything the chart finished before column k -- the tails Y[:, j]
+    and tau_j for j < k, and rows i < k of R -- is unaffected by that choice."""
+    dx = torch.sign(torch.diagonal(Hx, dim1=-2, dim2=-1))
+    dy = torch.sign(torch.diagonal(Hy, dim1=-2, dim2=-1))
+    dis = dx != dy
+    n = Hx.shape[-1]
+    first = dis.to(torch.int64).argmax(dim=-1)
+    return torch.where(dis.any(dim=-1), first, torch.full_like(first, n))
+
+
+def _elementwise_prefix(A, H, tau, near_tie=1e-4, min_prefix=0.5):
+    """Elementwise errors over the columns where the HIP path, the oracle and the closed form
+    take the same sign-rule choices.
+
+    Returns (errors of HIP vs exact, errors of oracle vs exact, HIP vs oracle), each as
+    (R scaled by max|A|, Y, tau).  A sign difference is allowed only at a near-tie, a column
+    whose live diagonal d_k (the oracle's) is below `near_tie` in magnitude: there the sign
+    is not determined by the data at fp32 precision.  Comparison stops before such a column,
+    which must leave at least `min_prefix` of the columns on average."""
+    Ho, to, d = orc.custom_kernel(A, return_diag=True)
+    Hc, tc = closed_form.geqrf_postmapped(A)
+    n = A.shape[-1]
+    k = torch.minimum(torch.minimum(_first_sign_change(H, Ho), _first_sign_change(H, Hc.float())),
+                      _first_sign_change(Ho, Hc.float()))
+    for b in range(A.shape[0]):
+        if int(k[b]) < n:
+            assert abs(float(d[b, k[b]])) < near_tie, (b, int(k[b]), float(d[b, k[b]]))
+    assert k.double().mean().item() >= min_prefix * n, k
+    idx = torch.arange(n)
+    rows = (idx.view(1, n, 1) < k.view(-1, 1, 1))   # rows i < k (R)
+    cols = (idx.view(1, 1, n) < k.view(-1, 1, 1))   # columns j < k (Y)
+    tcols = idx.view(1, n) < k.view(-1, 1)
+    scale = A.abs().amax(dim=(-2, -1), keepdim=True).double()
+
+    def errs(Hx, tx, Hy, ty):
+        Hx, tx, Hy, ty = Hx.double(), tx.double(), Hy.double(), ty.double()
+        eR = (((torch.triu(Hx) - torch.triu(Hy)) / scale).abs() * rows).max().item()
+        eY = ((torch.tril(Hx, -1) - torch.tril(Hy, -1)).abs() * cols).max().item()
+        et = ((tx - ty).abs() * tcols).max().item()
+        return eR, eY, et
+
+    return errs(H, tau, Hc, tc), errs(Ho, to, Hc, tc), errs(H, tau, Ho, to), k
+
+
+@pytest.mark.parametrize("n,seed", [(640, 3), (1100, 0), (2048, 1)])
+def test_large_n_elementwise_parity_split_form(rnr, wl, n, seed):
+    """Well-conditioned batches of 4 at n > 512: the split form (one launch per LU / chart
+    panel with multi-workgroup trailing updates, the per-block Cholesky launches, 64-row solve
+    blocks), against the oracle and the closed form elementwise."""
+    A = wl.well_conditioned(4, n, seed=100 * n + seed)
+    H, tau = _run(rnr, A)
+    _gates(A, H, tau, f"split n={n}")
+    e_hip, e_ref, d_ro, k = _elementwise_prefix(A, H, tau)
+    print(f"n={n} hip-exact {e_hip} oracle-exact {e_ref} hip-oracle {d_ro} prefix {k.tolist()}")
+    for eh, er in zip(e_hip, e_ref):
+        assert eh <= 4 * er + 1e-6, (n, e_hip, e_ref)
+    assert max(d_ro) < 5e-4, (n, d_ro)
+
+
+@pytest.mark.parametrize("n,seed", [(640, 3), (1100, 0), (2048, 1)])
+def test_large_n_elementwise_parity_fused_form(rnr, wl, n, seed):
+    """The same matrices inside a batch of 130, which takes the one-workgroup-per-matrix form
+    (32-wide LU / chart panels at n <= 1024, 16-wide with four rows per thread above; the
+    fused Cholesky; 128-row solve blocks): the first four against the oracle and the closed
+    form elementwise."""
+    A = wl.well_conditioned(4, n, seed=100 * n + seed)
+    big = torch.cat([A, A[:2].repeat(63, 1, 1)])
+    print(f"[case] fused form n={n} batch={big.shape[0]}", flush=True)
+    Hb, tb = rnr.custom_kernel(big.to(DEV))
+    torch.cuda.synchronize()
+    H, tau = Hb[:4].cpu(), tb[:4].cpu()
+    del Hb, tb
+    _gates(A, H, tau, f"fused n={n}")
+    e_hip, e_ref, d_ro, k = _elementwise_prefix(A, H, tau)
+    print(f"n={n} hip-exact {e_hip} oracle-exact {e_ref} hip-oracle {d_ro} prefix {k.tolist()}")
+    for eh, er in zip(e_hip, e_ref):
+        assert eh <= 4 * er + 1e-6, (n, e_hip, e_ref)
+    assert max(d_ro) < 5e-4, (n, d_ro)
+
+
 @pytest.mark.parametrize("b,n", [(6, 16), (8, 32), (6, 64), (4, 100), (4, 128), (2, 256), (2, 512)])
 def test_well_conditioned_elementwise_parity(rnr, wl, b, n):
     A = wl.well_conditioned(b, n, seed=1000 + n)
@@ -109,12 +193,18 @@ def test_headline_classes_pass_the_gates(rnr, wl, cls, n):
 
 
 def test_config1_cpu_plumbing_batch(rnr, wl):
+    """Configuration 1 (16 x 64, N(0, 1)): layout, gates, and H and tau elementwise against
+    the oracle and the closed form (the inputs are not conditioned on purpose, so the bound
+    is relative: at most 4x the oracle's own distance from the exact answer)."""
     A = wl.make_batch(1)
     H, tau = _run(rnr, A)
     assert H.shape == (16, 64, 64) and tau.shape == (16, 64) and H.dtype == torch.float32
     _gates(A, H, tau, "config1")
-    Ho, to = orc.custom_kernel(A)
-    assert (tau - to).abs().max().item() < 1e-3
+    e_hip, e_ref, d_ro, k = _elementwise_prefix(A, H, tau, min_prefix=0.9)
+    print(f"config1 hip-exact {e_hip} oracle-exact {e_ref} hip-oracle {d_ro}")
+    for eh, er in zip(e_hip, e_ref):
+        assert eh <= 4 * er + 1e-6, (e_hip, e_ref)
+    assert max(d_ro) < 1e-3, d_ro
 
 
 def test_config2_small_n_full_batch(rnr, wl):
@@ -273,6 +363,22 @@ def test_stage_cholqr_matches_oracle(rnr, wl, n):
     assert (Q - Qo).abs().max().item() < 2e-4
     eye = torch.eye(n, dtype=torch.float64)
     assert (Q.mT @ Q - eye).abs().max().item() < 1e-3
+
+
+@pytest.mark.parametrize("n", [24, 100, 512, 700])
+def test_stage_frame_matches_oracle_frame(rnr, wl, n):
+    """Q itself, not only its properties: the frame is unique (same pivots as getrf, positive
+    Cholesky diagonals), so the HIP Q must be at most 4x (plus 1e-6) further from the float64
+    frame than the oracle's fp32 Q is, and within 2e-4 of the oracle's."""
+    A = wl.well_conditioned(2, n, seed=3 * n + 2)
+    print(f"[case] frame vs oracle n={n}", flush=True)
+    Q = rnr._frame(A.to(DEV)).cpu().double()
+    Qo = orc.frame(A).double()
+    Qx = orc.frame(A.double())
+    e_hip = (Q - Qx).abs().max().item()
+    e_ref = (Qo - Qx).abs().max().item()
+    assert e_hip <= 4 * e_ref + 1e-6, (n, e_hip, e_ref)
+    assert (Q - Qo).abs().max().item() < 2e-4
 
 
 @pytest.mark.parametrize("n", [24, 200, 512])

@@ -230,3 +230,57 @@ def test_config1_batch_layout_and_gates(workloads):
     assert bool(ok.all())
     # margins well inside the gates, in line with the reference's README:93-105 table
     assert fr < ft / 100 and og < ot / 100
+
+
+def test_checker_fails_nan_like_the_reference():
+    """A NaN anywhere in H or tau fails the gates: the reference compares with `<`, which is
+    False for NaN (common/oracle.py:166-168).  The GPU checker must do the same."""
+    A = _randn(3, 24, 9).float()
+    Hg, tg = torch.geqrf(A.double())
+    H, tau = Hg.float(), tg.float()
+    H[0, 2, 5] = float("nan")       # in R
+    H[1, 9, 3] = float("nan")       # in a reflector tail
+    tau[2, 4] = float("nan")
+    fr, og, ft, ot, ok = checker.check(A, H, tau)
+    assert not bool(ok.any())
+    ratio, og2, okc = checker.check_percol(A, H, tau)
+    assert not bool(okc.any())
+
+
+def test_stress_cases_have_their_structure(workloads):
+    """The nine cases of the reference's stress battery (common/oracle.py:43-146)."""
+    n = 40
+    for case in workloads.STRESS_CASES:
+        A = workloads.stress_batch(case, 8, n, seed=3)
+        assert A.shape == (8, n, n) and A.dtype == torch.float32 and bool(torch.isfinite(A).all()), case
+        s = torch.linalg.svdvals(A.double())
+        if case == "rankdef":
+            assert s[:, n // 2:].max().item() < 1e-5 and s[:, : n // 2].min().item() > 0.09
+        elif case == "nearrank":
+            assert (s[:, n // 2:] - 1e-8).abs().max().item() < 1e-6
+        elif case == "clustered":
+            assert (s[:, : n // 2] - 1).abs().max().item() < 1e-5 and s[:, n // 2:].max().item() < 1e-5
+        elif case == "banded":
+            i = torch.arange(n)
+            assert A[:, (i.view(n, 1) - i.view(1, n)).abs() > n // 8].abs().max().item() == 0.0
+        elif case == "nearcollinear":
+            assert (A[:, :, 1] - A[:, :, 0]).abs().max().item() < 1e-5
+        elif case == "uppertri":
+            assert torch.equal(A, torch.triu(A))
+        elif case == "mixed":  # matrices 3 and 7 are stress cases: rankdef, then nearrank
+            assert torch.linalg.svdvals(A[3].double())[n // 2:].max().item() < 1e-5
+            assert torch.linalg.svdvals(A[7].double())[n // 2:].max().item() < 1e-6
+    # seeded: the same call twice gives the same batch, another seed another one
+    assert torch.equal(workloads.stress_batch("dense", 2, 16, seed=5), workloads.stress_batch("dense", 2, 16, seed=5))
+    assert not torch.equal(workloads.stress_batch("dense", 2, 16, seed=5), workloads.stress_batch("dense", 2, 16, seed=6))
+
+
+@pytest.mark.parametrize("case", ["dense", "mixed", "rankdef", "nearrank", "clustered", "banded", "rowscaled",
+                                  "nearcollinear", "uppertri"])
+def test_oracle_passes_the_stress_battery(case, workloads):
+    """The reference algorithm (oracle) passes the per-column gate on every stress case."""
+    A = workloads.stress_batch(case, 8, 64, seed=0)
+    H, tau = rnr.custom_kernel(A)
+    ratio, og, ok = checker.check_percol(A, H, tau)
+    assert bool(ok.all()), (case, ratio, og)
+    assert tau.min().item() >= 1.0 - 16 * EPS32 and tau.max().item() <= 2.0
