@@ -46,7 +46,8 @@ enum rnr_status {
   RNR_ERR_UNSUPPORTED_N = 2,  /* n outside [1, RNR_MAX_N] */
   RNR_ERR_WORKSPACE = 3,      /* workspace pointer null or smaller than the query result */
   RNR_ERR_HIP = 4,            /* a HIP launch or attribute call failed */
-  RNR_ERR_MISALIGNED = 5      /* a pointer is not 4-byte aligned (workspace: 256-byte) */
+  RNR_ERR_MISALIGNED = 5,     /* a pointer is not 4-byte aligned (workspace: 256-byte) */
+  RNR_ERR_SCRATCH_LIMIT = 6   /* rnr_qr_f32_noalloc: the problem needs more than its scratch */
 };
 
 #define RNR_MAX_N 2048
@@ -72,6 +73,20 @@ int rnr_qr_f32_workspace(int64_t batch, int64_t n, size_t* bytes);
 int rnr_qr_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride,
                float* H, float* tau, int32_t* info,
                void* ws, size_t ws_bytes, rnr_stream_t stream);
+
+/* rnr_qr_f32 for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Takes no workspace and calls no allocating routine: the workspace lives in a device array
+ * of RNR_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on until the
+ * process ends.  Problems whose workspace (rnr_qr_f32_workspace) exceeds it return
+ * RNR_ERR_SCRATCH_LIMIT before any launch: at n = 512 up to 31 matrices per call, at
+ * n = 1024 up to 7, at n = 2048 one; n <= 64 needs none.  All calls on one GPU share its
+ * array, so calls that overlap on one GPU (other streams, other host threads) race and must
+ * be ordered by the caller.  Nothing in it needs to start at zero.  Results equal
+ * rnr_qr_f32's bit for bit. */
+#define RNR_NOALLOC_SCRATCH_BYTES (128u << 20)
+int rnr_qr_f32_noalloc(const float* A, int64_t batch, int64_t n, int64_t batch_stride,
+                       float* H, float* tau, int32_t* info, rnr_stream_t stream);
 
 /* Same as rnr_qr_f32, and records events[i] (hipEvent_t handles created by the caller) on
  * the stream before stage i of the sequence and events[11] after the last, for per-kernel

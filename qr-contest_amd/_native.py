@@ -19,6 +19,8 @@ RNR_ERR_UNSUPPORTED_N = 2
 RNR_ERR_WORKSPACE = 3
 RNR_ERR_HIP = 4
 RNR_ERR_MISALIGNED = 5
+RNR_ERR_SCRATCH_LIMIT = 6
+RNR_NOALLOC_SCRATCH_BYTES = 128 << 20
 RNR_MAX_N = 2048
 RNR_QR_TIMED_EVENTS = 12
 # the stages of rnr_qr_f32 in order (what rnr_qr_f32_timed's events bracket)
@@ -38,6 +40,7 @@ SIGNATURES = {
     "rnr_version": (ctypes.c_char_p, []),
     "rnr_qr_f32_workspace": (_int, [_i64, _i64, _szp]),
     "rnr_qr_f32": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "rnr_qr_f32_noalloc": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "rnr_qr_f32_timed": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp,
                                 ctypes.POINTER(ctypes.c_void_p), _int]),
     "rnr_lu_f32_workspace": (_int, [_i64, _i64, _szp]),

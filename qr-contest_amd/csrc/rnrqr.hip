@@ -19,6 +19,8 @@
 //
 // For n <= kSmallMaxN (64) the whole path is instead one launch of k_small (small.hpp), one
 // matrix per group of lanes of a wave; it needs no workspace.
+#include <mutex>
+
 #include "../../include/rnrqr.h"
 #include "common.hpp"
 #include "gemm_tn.hpp"
@@ -367,6 +369,36 @@ int qr_path(const float* A, int64_t batch, int64_t n, int64_t batch_stride, floa
   return mk.mark(st);
 }
 
+// ---- scratch of the allocation-free entry point (rnr_qr_f32_noalloc) -----------------------
+// One file-scope device array per GPU, held from the code object's load to the end of the
+// process.  Host code never uses the array's name as an address (in host code it is only a
+// stand-in for the symbol): the device address comes from hipGetSymbolAddress, looked up once
+// per device with that device current, and is kept per device.
+static __device__ __align__(256) unsigned char scratch[RNR_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch address on the stream's device (looked up on the first call there).
+int scratch_on(hipStream_t st, void** out) {
+  int dev = -1;
+  if (hipStreamGetDevice(st, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return RNR_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return RNR_ERR_HIP;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return RNR_ERR_HIP;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev && hipSetDevice(cur) != hipSuccess) return RNR_ERR_HIP;
+    if (e != hipSuccess || !p) return RNR_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return RNR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -379,6 +411,9 @@ const char* rnr_status_string(int status) {
     case RNR_ERR_WORKSPACE: return "workspace missing or smaller than the size query returned";
     case RNR_ERR_HIP: return "HIP launch or attribute call failed";
     case RNR_ERR_MISALIGNED: return "misaligned pointer (data: 4 bytes, workspace: 256 bytes)";
+    case RNR_ERR_SCRATCH_LIMIT:
+      return "the problem needs more scratch than rnr_qr_f32_noalloc holds (RNR_NOALLOC_SCRATCH_BYTES, "
+             "128 MiB per GPU); use rnr_qr_f32 with a workspace, or a smaller batch";
     default: return "unknown status";
   }
 }
@@ -397,6 +432,20 @@ int rnr_qr_f32(const float* A, int64_t batch, int64_t n, int64_t batch_stride, f
   Marks mk{nullptr, 0, 0};
   return qr_path(A, batch, n, batch_stride, H, tau, info, ws, ws_bytes,
                  reinterpret_cast<hipStream_t>(stream), mk);
+}
+
+int rnr_qr_f32_noalloc(const float* A, int64_t batch, int64_t n, int64_t batch_stride, float* H, float* tau,
+                       int32_t* info, rnr_stream_t stream) {
+  if (int e = check_common(batch, n)) return e;
+  if (batch == 0) return RNR_OK;
+  const size_t need = small_path(n) ? 0 : carve(batch, n, kQrNeed, nullptr, nullptr);
+  if (need > (size_t)RNR_NOALLOC_SCRATCH_BYTES) return RNR_ERR_SCRATCH_LIMIT;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if (need > 0)
+    if (int e = scratch_on(st, &ws)) return e;
+  Marks mk{nullptr, 0, 0};
+  return qr_path(A, batch, n, batch_stride, H, tau, info, ws, need, st, mk);
 }
 
 int rnr_qr_f32_timed(const float* A, int64_t batch, int64_t n, int64_t batch_stride, float* H,

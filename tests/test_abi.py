@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib, native):
 
 
 def test_status_strings(lib, native):
-    for code in range(6):
+    for code in range(7):
         assert native.status_string(code)
     assert native.status_string(0) == "success"
     assert "unknown" in native.status_string(99)
@@ -165,3 +165,15 @@ def test_build_command_targets_gfx950_without_packed_fp32(pkg):
     assert "--offload-arch=gfx950" in cmd
     i = cmd.index("-packed-fp32-ops")
     assert cmd[i - 1] == "-Xclang" and cmd[i - 2] == "-target-feature"
+
+
+def test_noalloc_entry_rejects_before_touching_the_gpu(lib, native):
+    """rnr_qr_f32_noalloc validates sizes on the host before it looks up its scratch or
+    launches: a problem whose workspace exceeds RNR_NOALLOC_SCRATCH_BYTES is refused."""
+    f = lib.rnr_qr_f32_noalloc
+    fake = 1 << 20
+    assert f(fake, 32, 512, 512 * 512, fake, fake, None, None) == native.RNR_ERR_SCRATCH_LIMIT
+    assert f(fake, 2, 2048, 2048 * 2048, fake, fake, None, None) == native.RNR_ERR_SCRATCH_LIMIT
+    assert f(fake, 4, 2049, 2049 * 2049, fake, fake, None, None) == native.RNR_ERR_UNSUPPORTED_N
+    assert f(fake, -1, 8, 64, fake, fake, None, None) == native.RNR_ERR_INVALID_ARG
+    assert f(None, 0, 100, 0, None, None, None, None) == native.RNR_OK  # empty batch: nothing to do
