@@ -38,7 +38,7 @@ constexpr int kCholNb = 64;
 
 inline size_t chol_lds_bytes(int n, bool strip) {
   const size_t w = n > kCholNb ? (size_t)(n - kCholNb) : 1;
-  return sizeof(float) * (64 * 65 + 64 * 68 + 64 + 64 + 32 + (strip ? 64 * w + 64 : 0));
+  return sizeof(float) * (64 * 65 + 64 * 68 + 64 + 128 + 32 + (strip ? 64 * w + 64 : 0));
 }
 
 // Wave 0: factor the 64x64 diagonal block held in D (symmetric; the upper part is read) in
@@ -47,10 +47,13 @@ inline size_t chol_lds_bytes(int n, bool strip) {
 // (column index, or INT_MAX).  Lane i holds symmetric row i of the block in four named
 // 16-wide vectors (compile-time element access keeps them in VGPRs).  Step j: lane c holds
 // G'[j][c] = G'[c][j], so the scaled pivot row R[j][c] = G'[j][c] / r sits in lane c; it is
-// broadcast through one LDS row SB, all of whose reads issue together (one round trip per
-// step).  A wave issues its LDS operations in order; wave_lds_order keeps the compiler from
-// moving them, so no barrier sits on the chain.  The pivot's square root and reciprocal are
-// the hardware's (1 ulp).
+// broadcast through an LDS row SB[j % 2] (two rows: SB holds 2 x 64 floats), all of whose
+// reads issue together.  The steps are software-pipelined: step j first updates column j + 1
+// only, which is all step j + 1's pivot needs, then forms step j + 1's pivot and issues its
+// broadcast, and only then updates its remaining columns -- so step j + 1's LDS round trip
+// runs under step j's FMAs instead of after them.  A wave issues its LDS operations in order;
+// wave_lds_order keeps the compiler from moving them, so no barrier sits on the chain.  The
+// pivot's square root and reciprocal are the hardware's (1 ulp).
 __device__ __forceinline__ int chol_diag_wave(float* D, float* RT, float* RI, float* SB, int lane) {
   asm volatile("" : "+v"(lane));  // lane-derived values stay here, not hoisted out of the caller's loop
   f32x16 v0, v1, v2, v3;
@@ -70,45 +73,66 @@ __device__ __forceinline__ int chol_diag_wave(float* D, float* RT, float* RI, fl
       v[e] = D[(c >= lane) ? lane * 65 + c : c * 65 + lane];
     }
   });
+  // v[c] -= sm * pv for one compile-time column c
+  auto upd = [&](auto cc, float sm, float pv) {
+    constexpr int c = decltype(cc)::value;
+    V(std::integral_constant<int, c / 16>{})[c % 16] -= sm * pv;
+  };
   int fail = INT_MAX;
-  static_for<0, 64>([&](auto jc) {
+  // head of step j: the pivot (column j, already final), this lane's scaled row value si and
+  // update multiplier sm, the broadcast into SB[j % 2]
+  float si = 0.f, sm = 0.f, rinv = 0.f;
+  auto head = [&](auto jc) {
     constexpr int j = decltype(jc)::value;
-    constexpr int C0 = (j + 1) / 4;
     int ln = lane;
     asm volatile("" : "+v"(ln));
     const float rjj = V(std::integral_constant<int, j / 16>{})[j % 16];
     const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rjj), j));
     if (!(d > 0.f) && fail == INT_MAX) fail = j;
-    const float r = __builtin_amdgcn_sqrtf(d), rinv = __builtin_amdgcn_rcpf(r);
-    const float si = (ln == j) ? r : rjj * rinv;  // lane c > j: R[j][c]
-    const float sm = (ln > j) ? si : 0.f;          // rows below j take the update
-    SB[ln] = si;
+    const float r = __builtin_amdgcn_sqrtf(d);
+    rinv = __builtin_amdgcn_rcpf(r);
+    si = (ln == j) ? r : rjj * rinv;  // lane c > j: R[j][c]
+    sm = (ln > j) ? si : 0.f;         // rows below j take the update
+    SB[(j & 1) * 64 + ln] = si;
     wave_lds_order();
-    if constexpr (C0 < 16) {
-      float4 p[16 - C0];
-      const lds_f4* sbp = lds_base(SB);
+  };
+  // the broadcast row of the current step (float4 units from column 4 * ((j + 1) / 4) on)
+  float4 pc[16];
+  auto read_row = [&](auto jc, float4 (&dst)[16]) {
+    constexpr int j = decltype(jc)::value;
+    constexpr int C0 = (j + 1) / 4;
+    const lds_f4* sbp = lds_base(SB + (j & 1) * 64);
 #pragma unroll
-      for (int c4 = C0; c4 < 16; ++c4) p[c4 - C0] = lds_get(sbp, c4);
-#pragma unroll
-      for (int c4 = C0; c4 < 16; ++c4) {
-        const float pv[4] = {p[c4 - C0].x, p[c4 - C0].y, p[c4 - C0].z, p[c4 - C0].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int c = 4 * c4 + e;
-          if (c > j) {
-            if (c < 16) v0[c] -= sm * pv[e];
-            else if (c < 32) v1[c - 16] -= sm * pv[e];
-            else if (c < 48) v2[c - 32] -= sm * pv[e];
-            else v3[c - 48] -= sm * pv[e];
-          }
-        }
-      }
-    }
+    for (int c4 = C0; c4 < 16; ++c4) dst[c4] = lds_get(sbp, c4);
+  };
+  auto pget = [&](const float4 (&row)[16], auto cc) -> float {
+    constexpr int c = decltype(cc)::value;
+    return f4get<c % 4>(row[c / 4]);
+  };
+  head(std::integral_constant<int, 0>{});
+  read_row(std::integral_constant<int, 0>{}, pc);
+  static_for<0, 64>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    // row j of R from this step's values (lane ln: R[j][ln])
     const float rj = (ln >= j) ? si : 0.f;
+    const float smj = sm, rinvj = rinv;
+    if constexpr (j + 1 < 64) {
+      // column j + 1 first: step j + 1's pivot and broadcast depend on it alone
+      upd(std::integral_constant<int, j + 1>{}, smj, pget(pc, std::integral_constant<int, j + 1>{}));
+      head(std::integral_constant<int, j + 1>{});
+      float4 pn[16];
+      read_row(std::integral_constant<int, j + 1>{}, pn);  // in flight during the rest of step j
+      // the rest of step j's update
+      static_for<j + 2, 64>([&](auto cc) { upd(cc, smj, pget(pc, cc)); });
+#pragma unroll
+      for (int c4 = (j + 2) / 4; c4 < 16; ++c4) pc[c4] = pn[c4];
+    }
     D[j * 65 + ln] = rj;   // row j of R
     RT[ln * 68 + j] = rj;  // column ln of R
-    RI[j] = rinv;          // same value from every lane
-    wave_lds_order();      // the next step's SB store stays behind this step's reads
+    RI[j] = rinvj;         // same value from every lane
+    wave_lds_order();      // a later step's SB store stays behind this step's reads
   });
   return fail;
 }
@@ -174,8 +198,8 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
   float* XT = D + 64 * 65;         // [64][65] (R_kk^-1)^T: XT[i][k] = Dinv_kk[k][i] ...
   float* RT = XT;                  // ... over [64][68] R_kk column-major while it is factored
   float* RI = XT + 64 * 68;        // [64] 1 / R[j][j] of the diagonal block
-  float* SB = RI + 64;             // [64] scaled pivot row broadcast (wave 0)
-  float* red = SB + 64;            // [16]
+  float* SB = RI + 64;             // [2][64] scaled pivot row broadcasts (wave 0)
+  float* red = SB + 128;           // [16]
   int* ffail = reinterpret_cast<int*>(red + 16);
   float* S = red + 32;             // block row [64][n-64] when strip_lds
 
@@ -230,6 +254,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
         float bv[32];
 #pragma unroll
         for (int t = 0; t < 32; ++t) bv[t] = G[base + 2 * t * n];
+        issue_loads_first();
         f32x16 acc0 = zero16(), acc1 = zero16();
 #pragma unroll
         for (int t = 0; t < 32; ++t) {
@@ -273,6 +298,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
           const int col = min(k1 + 32 * qj + l32, n - 1);
           q[r] = G[row * n + col];
         }
+        issue_loads_first();
         const int ci = 32 * qi + l32, cj = 32 * qj + l32;
         if (a.strip_lds) {
 #pragma unroll 8
@@ -329,6 +355,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
               const int col = min(k1 + J * 64 + nj * 32 + l32, n - 1);
               acc[mi][nj][r] = G[row * n + col];
             }
+        issue_loads_first();
         if (!first) {
           // Operand reads are unconditional: a row ci >= w of R_k,> only meets accumulator
           // rows (or columns) >= w of this tile, which are never stored.  The strip has 64
@@ -429,7 +456,7 @@ __global__ __launch_bounds__(64) void k_chol_diag(CholSplitArgs a) {
   __shared__ float D[64 * 65];
   __shared__ __attribute__((aligned(16))) float XT[64 * 68];  // RT while factoring, then XT
   __shared__ float RI[64];
-  __shared__ float SB[64];
+  __shared__ __attribute__((aligned(16))) float SB[128];
   const int n = a.n, k0 = a.k0, b = blockIdx.x, lane = threadIdx.x;
   const int kb = min(kCholNb, n - k0);
   float* G = a.G + b * a.sg;
@@ -476,6 +503,7 @@ __global__ __launch_bounds__(kCholSplitThreads) void k_chol_row(CholSplitArgs a)
   float bv[32];
 #pragma unroll
   for (int t = 0; t < 32; ++t) bv[t] = G[base + 2 * t * n];
+  issue_loads_first();
   constexpr int DPT = 64 * 64 / kCholSplitThreads;
   float dv[DPT];
 #pragma unroll
@@ -530,6 +558,7 @@ __global__ __launch_bounds__(kCholSplitThreads) void k_chol_trail(CholSplitArgs 
         const int col = min(k1 + J * 64 + nj * 32 + l32, n - 1);
         acc[mi][nj][r] = G[row * n + col];
       }
+  issue_loads_first();
   const int ci0 = I * 64 + l32, cj0 = J * 64 + l32;  // reads past w reach unstored entries only
 #pragma unroll
   for (int kk = 0; kk < kCholNb; kk += 2) {

@@ -38,6 +38,11 @@ __device__ __forceinline__ int xcd_remap(int pid, int total) {
   return (pid % kXcd) * per + pid / kXcd;
 }
 
+// Keeps the loads issued above this point ahead of everything below it.  Left alone, the
+// scheduler interleaves a block of independent loads with their consumers (MFMAs), so each
+// consumer waits on a load issued just before it instead of all loads sharing one latency.
+__device__ __forceinline__ void issue_loads_first() { __builtin_amdgcn_sched_barrier(0); }
+
 // Orders LDS traffic between lanes of one wave (a wave executes its LDS operations in
 // program order; this keeps the compiler from moving loads above earlier stores).
 __device__ __forceinline__ void wave_lds_order() {
