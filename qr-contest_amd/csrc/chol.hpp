@@ -191,8 +191,12 @@ __device__ __forceinline__ void chol_inverse_wave(const float* RT, const float* 
   for (int r = 0; r < 16; ++r) XT[(32 + l32) * 65 + acc_row(r, lane)] = x12[r];
 }
 
-__global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
-  constexpr int NW = kCholThreads / 64;
+// T: threads per workgroup (512; 256 for n <= 256, where more waves would mostly idle; the
+// next diagonal tile's quadrants need waves 0, 1 and 3).
+template <int T = kCholThreads>
+__global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_chol(CholArgs a) {
+  static_assert(T >= 256, "the diagonal-tile quadrants run on waves 0, 1 and 3");
+  constexpr int NW = T / 64;
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float* D = smem;                 // [64][65] diagonal block, then R_kk (upper, zero below)
   float* XT = D + 64 * 65;         // [64][65] (R_kk^-1)^T: XT[i][k] = Dinv_kk[k][i] ...
@@ -212,7 +216,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
 
   // jitter
   float part = 0.f;
-  for (int i = tid; i < n; i += kCholThreads) part += G[(int64_t)i * n + i];
+  for (int i = tid; i < n; i += T) part += G[(int64_t)i * n + i];
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
   if (lane == 0) red[wid] = part;
@@ -222,7 +226,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
 #pragma unroll
   for (int w = 0; w < NW; ++w) tot += red[w];
   const float mu = 1e-7f * (tot / (float)n);
-  for (int i = tid; i < n; i += kCholThreads) G[(int64_t)i * n + i] += mu;
+  for (int i = tid; i < n; i += T) G[(int64_t)i * n + i] += mu;
   __syncthreads();
 
   // Iteration k0 = -64 has no block of its own: its "trailing update" is wave 0 taking the
@@ -233,7 +237,7 @@ __global__ __launch_bounds__(kCholThreads) void k_chol(CholArgs a) {
 
     if (!first) {
       // R_kk (upper) and Dinv_kk (row-major, zero below the diagonal) to HBM
-      for (int idx = tid; idx < kb * 64; idx += kCholThreads) {
+      for (int idx = tid; idx < kb * 64; idx += T) {
         const int i = idx >> 6, c = idx & 63;
         if (c < kb && c >= i) G[(k0 + i) * n + k0 + c] = D[i * 65 + c];
         Dv[(k0 + i) * 64 + c] = (c < kb) ? XT[c * 65 + i] : 0.f;

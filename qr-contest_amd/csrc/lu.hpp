@@ -58,11 +58,11 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
 inline int lu_panel_nb(int n) { return n <= 512 ? 64 : (n <= 1024 ? 32 : 16); }
 
 // panel [n][nb+1] | -U12 chunk [nb][64] | row map [n] | pivot keys [3] (u64) | per-wave
-// candidate slots [2][8][nb+4]
-inline size_t lu_lds_bytes(int n, int nb, bool direct = false) {
+// candidate slots [2][nw][nb+4] (nw = waves per workgroup)
+inline size_t lu_lds_bytes(int n, int nb, bool direct = false, int nw = 8) {
   const size_t p = ((size_t)(direct ? nb : n) * (nb + 1) + 3) & ~(size_t)3;
   const size_t pl = ((size_t)n + 3) & ~(size_t)3;
-  return sizeof(float) * (p + (size_t)nb * 64 + pl + 8 + 2 * 8 * (size_t)(nb + 4));
+  return sizeof(float) * (p + (size_t)nb * 64 + pl + 8 + 2 * (size_t)nw * (size_t)(nb + 4));
 }
 
 // SPLIT = true: one launch factors only panel a.k0 and stops before its trailing update,
@@ -124,9 +124,11 @@ __device__ __forceinline__ void lu_inverse_wave(float* P, const float* LT, int l
   for (int r = 0; r < 16; ++r) P[(32 + acc_row(r, lane)) * LDP + l32] = x21[r];
 }
 
-template <bool PIVOT, int NB, int RPT, bool SPLIT = false>
-__global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
-  constexpr int T = kLuThreads, NW = T / 64;
+// T: threads per workgroup (512; 128 or 256 for n <= 128 / 256 with 64-wide panels, so that
+// small matrices do not hold idle waves and several workgroups share a CU).
+template <bool PIVOT, int NB, int RPT, bool SPLIT = false, int T = kLuThreads>
+__global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_lu(LuArgs a) {
+  constexpr int NW = T / 64;
   constexpr int NB4 = NB / 4;
   constexpr int LDP = NB + 1;
   constexpr int CPW = NB / NW;       // columns of L11^-1 per wave
@@ -500,30 +502,34 @@ __global__ __launch_bounds__(kLuThreads) void k_lu(LuArgs a) {
       {
         // a wave's jobs load their A12 columns first, then multiply: one load latency per
         // chunk instead of one per job
-        constexpr int NBI = NB / 16, NJOB = NBI * 4, JPW = (NJOB + NW - 1) / NW;
-        float bv[JPW][NB4];
+        // (in rounds of at most two jobs per wave: few waves would otherwise hold many rows)
+        constexpr int NBI = NB / 16, NJOB = NBI * 4, JPW = (NJOB + NW - 1) / NW, JPR = JPW < 2 ? JPW : 2;
 #pragma unroll
-        for (int u = 0; u < JPW; ++u) {
-          const int job = wid + u * NW, bj = job & 3;
-          const int col = c0 + bj * 16 + l16;
+        for (int u0 = 0; u0 < JPW; u0 += JPR) {
+          float bv[JPR][NB4];
 #pragma unroll
-          for (int t = 0; t < NB4; ++t) {
-            const int k = 4 * t + q4;
-            const int pr = PIVOT ? pl[k0 + k] : k0 + k;
-            bv[u][t] = (job < NJOB) ? cur[(int64_t)pr * n + min(col, n - 1)] : 0.f;  // columns past n: unstored
+          for (int u = 0; u < JPR; ++u) {
+            const int job = wid + (u0 + u) * NW, bj = job & 3;
+            const int col = c0 + bj * 16 + l16;
+#pragma unroll
+            for (int t = 0; t < NB4; ++t) {
+              const int k = 4 * t + q4;
+              const int pr = PIVOT ? pl[k0 + k] : k0 + k;
+              bv[u][t] = (job < NJOB) ? cur[(int64_t)pr * n + min(col, n - 1)] : 0.f;  // columns past n: unstored
+            }
           }
-        }
 #pragma unroll
-        for (int u = 0; u < JPW; ++u) {
-          const int job = wid + u * NW;
-          if (job < NJOB) {
-            const int bi = job >> 2, bj = job & 3;
-            const int i = bi * 16 + l16;
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          for (int u = 0; u < JPR; ++u) {
+            const int job = wid + (u0 + u) * NW;
+            if (job < NJOB) {
+              const int bi = job >> 2, bj = job & 3;
+              const int i = bi * 16 + l16;
+              f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int t = 0; t < NB4; ++t) acc = mfma16(P[sw(i, 4 * t + q4)], bv[u][t], acc);
+              for (int t = 0; t < NB4; ++t) acc = mfma16(P[sw(i, 4 * t + q4)], bv[u][t], acc);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) U[(bi * 16 + 4 * q4 + r) * 64 + bj * 16 + l16] = -acc[r];
+              for (int r = 0; r < 4; ++r) U[(bi * 16 + 4 * q4 + r) * 64 + bj * 16 + l16] = -acc[r];
+            }
           }
         }
       }

@@ -105,12 +105,12 @@ int set_lds(K kernel, size_t bytes) {
              : RNR_ERR_HIP;
 }
 
-template <bool PIVOT, int NB, int RPT>
+template <bool PIVOT, int NB, int RPT, int T = kLuThreads>
 int launch_lu_nb(const LuArgs& a, int64_t batch, hipStream_t st) {
-  const size_t lds = lu_lds_bytes(a.n, NB);
+  const size_t lds = lu_lds_bytes(a.n, NB, false, T / 64);
   if (lds > kLdsMax) return RNR_ERR_UNSUPPORTED_N;
-  if (int e = set_lds(k_lu<PIVOT, NB, RPT>, lds)) return e;
-  k_lu<PIVOT, NB, RPT><<<dim3((unsigned)batch), dim3(kLuThreads), lds, st>>>(a);
+  if (int e = set_lds(k_lu<PIVOT, NB, RPT, false, T>, lds)) return e;
+  k_lu<PIVOT, NB, RPT, false, T><<<dim3((unsigned)batch), dim3(T), lds, st>>>(a);
   return hip_status();
 }
 
@@ -155,13 +155,21 @@ int launch_lu(bool pivot, const float* src, int64_t ss, float* dst, int64_t sd, 
     if (pivot) return n <= 1024 ? launch_lu_split<true, 32, 2>(a, batch, st) : launch_lu_split<true, 32, 4>(a, batch, st);
     return n <= 1024 ? launch_lu_split<false, 32, 2>(a, batch, st) : launch_lu_split<false, 32, 4>(a, batch, st);
   }
-  // rows per thread: n <= kLuThreads * RPT
+  // rows per thread: n <= T * RPT; one row per thread with 128 or 256 threads at n <= 128 / 256
   if (pivot) {
-    if (nb == 64) return launch_lu_nb<true, 64, 1>(a, batch, st);
+    if (nb == 64) {
+      if (n <= 128) return launch_lu_nb<true, 64, 1, 128>(a, batch, st);
+      if (n <= 256) return launch_lu_nb<true, 64, 1, 256>(a, batch, st);
+      return launch_lu_nb<true, 64, 1>(a, batch, st);
+    }
     if (nb == 32) return launch_lu_nb<true, 32, 2>(a, batch, st);
     return launch_lu_nb<true, 16, 4>(a, batch, st);
   }
-  if (nb == 64) return launch_lu_nb<false, 64, 1>(a, batch, st);
+  if (nb == 64) {
+    if (n <= 128) return launch_lu_nb<false, 64, 1, 128>(a, batch, st);
+    if (n <= 256) return launch_lu_nb<false, 64, 1, 256>(a, batch, st);
+    return launch_lu_nb<false, 64, 1>(a, batch, st);
+  }
   if (nb == 32) return launch_lu_nb<false, 32, 2>(a, batch, st);
   return launch_lu_nb<false, 16, 4>(a, batch, st);
 }
@@ -241,8 +249,13 @@ int launch_chol(float* G, int64_t sg, float* Dinv, int* info, int64_t batch, int
   } else {
     a.strip_lds = chol_lds_bytes(n, true) <= kLdsMax ? 1 : 0;
     const size_t lds = chol_lds_bytes(n, a.strip_lds != 0);
-    if (int e = set_lds(k_chol, lds)) return e;
-    k_chol<<<dim3((unsigned)batch), dim3(kCholThreads), lds, st>>>(a);
+    if (n <= 256) {  // half the waves: the other half would mostly idle
+      if (int e = set_lds(k_chol<256>, lds)) return e;
+      k_chol<256><<<dim3((unsigned)batch), dim3(256), lds, st>>>(a);
+    } else {
+      if (int e = set_lds(k_chol<>, lds)) return e;
+      k_chol<><<<dim3((unsigned)batch), dim3(kCholThreads), lds, st>>>(a);
+    }
   }
   return hip_status();
 }
