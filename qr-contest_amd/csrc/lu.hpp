@@ -57,12 +57,12 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
 
 inline int lu_panel_nb(int n) { return n <= 512 ? 64 : (n <= 1024 ? 32 : 16); }
 
-// panel [n][nb+1] | -U12 chunk [nb][64] | row map [n] | pivot keys [3] (u64) | per-wave
-// candidate slots [2][nw][nb+4] (nw = waves per workgroup)
-inline size_t lu_lds_bytes(int n, int nb, bool direct = false, int nw = 8) {
+// panel [n][nb+1] | -U12 chunk [nb][64] | row map [n] | pivot keys [3] (u64) | pivot row
+// slots [2][nb+4]
+inline size_t lu_lds_bytes(int n, int nb, bool direct = false) {
   const size_t p = ((size_t)(direct ? nb : n) * (nb + 1) + 3) & ~(size_t)3;
   const size_t pl = ((size_t)n + 3) & ~(size_t)3;
-  return sizeof(float) * (p + (size_t)nb * 64 + pl + 8 + 2 * (size_t)nw * (size_t)(nb + 4));
+  return sizeof(float) * (p + (size_t)nb * 64 + pl + 8 + 2 * (size_t)(nb + 4));
 }
 
 // SPLIT = true: one launch factors only panel a.k0 and stops before its trailing update,
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_l
   int* pl = reinterpret_cast<int*>(U + NB * 64);    // logical -> physical row
   unsigned long long* pkeys =                       // [3] pivot keys (LU), by step mod 3
       reinterpret_cast<unsigned long long*>(reinterpret_cast<float*>(pl) + ((n + 3) & ~3));
-  float* slots = reinterpret_cast<float*>(pkeys) + 8;  // [2][NW][NB+4] candidate rows
+  float* slots = reinterpret_cast<float*>(pkeys) + 8;  // [2][NB+4] pivot rows, by column parity
 
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5, l16 = lane & 15, q4 = lane >> 4;
@@ -231,13 +231,14 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_l
       }
     }
 
-    // ---- factor the panel column by column (compile-time column index).  One barrier per
-    //      column.  Rows stay in their threads: pos[q] is the logical position (relative to
-    //      k0) of the row a thread holds, and a pivot choice only swaps two labels.  Each
-    //      wave publishes its best candidate key in one LDS atomic maximum and the candidate
-    //      row in a per-wave slot (double-buffered by column parity), so after the barrier
-    //      every thread finds the pivot and reads its row.  Waves whose rows all lie at or
-    //      past m (finished rows) only take part in the barriers.
+    // ---- factor the panel column by column (compile-time column index).  Rows stay in
+    //      their threads: pos[q] is the logical position (relative to k0) of the row a thread
+    //      holds, and a pivot choice only swaps two labels.  LU: each wave publishes its best
+    //      candidate key in one LDS atomic maximum; after a barrier the lane holding the
+    //      winning key stores its row in the pivot slot (double-buffered by column parity),
+    //      and after a second barrier every thread reads it.  Chart: the pivot row's thread
+    //      stores it, one barrier.  Waves whose rows all lie at or past m (finished rows)
+    //      only take part in the barriers.
     const int nwa = min(NW, (m + 63) >> 6);  // waves holding rows < m
     const bool wact = wid < nwa;
     int pos[RPT], phys[RPT];
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_l
         // kernel start (which spills ~1000 SGPRs)
         int rbase = tid;
         asm volatile("" : "+v"(rbase));
-        float4* sb = slot4 + buf * NW * SLOT4;
+        float4* sb = slot4 + buf * SLOT4;
         float4 pr4[NB4 - C0];
         float l[RPT];
         if constexpr (PIVOT) {
@@ -272,9 +273,9 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_l
           unsigned long long* kcur = pkeys + kb3;
           if (tid == 0) pkeys[kb3n] = 0ull;
           kb3 = kb3n;
+          uint64_t best = 0;
+          int bq = 0;
           if (wact) {
-            uint64_t best = 0;
-            int bq = 0;
 #pragma unroll
             for (int q = 0; q < RPT; ++q) {
               const int r = rbase + T * q;
@@ -285,33 +286,36 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_l
               if (key > best) { best = key; bq = q; }
             }
             const uint64_t wbest = wave_max_key(best);
-            if (best == wbest) {  // exactly one lane: keys are distinct
-              atomicMax(kcur, (unsigned long long)wbest);
-              // the winning row: one masked store block per row of the thread, only the winner's
-              // executing (the stored values pass through an empty asm so the blocks are not
-              // merged into a lane-dependent index into row[], which would put row[] on the stack)
+            if (best == wbest) atomicMax(kcur, (unsigned long long)wbest);  // one lane: keys are distinct
+          }
+          __syncthreads();
+          // only the winning lane publishes its row, between two barriers: LDS instructions cost
+          // their full wave width whatever the active lanes, so one wave storing beats every
+          // wave storing its own candidate
+          const uint64_t pk = *kcur;
+          if (wact && best == pk) {
+            // one masked store block per row of the thread, only the winner's executing (the
+            // stored values pass through an empty asm so the blocks are not merged into a
+            // lane-dependent index into row[], which would put row[] on the stack)
 #pragma unroll
-              for (int q = 0; q < RPT; ++q) {
-                if (RPT == 1 || bq == q) {
+            for (int q = 0; q < RPT; ++q) {
+              if (RPT == 1 || bq == q) {
 #pragma unroll
-                  for (int c4 = C0; c4 < NB4; ++c4) {
-                    float4 o = make_float4(row[q][4 * c4], row[q][4 * c4 + 1], row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
-                    if (RPT > 1) asm volatile("" : "+v"(o.x), "+v"(o.y), "+v"(o.z), "+v"(o.w));
-                    sb[wid * SLOT4 + 1 + c4] = o;
-                  }
+                for (int c4 = C0; c4 < NB4; ++c4) {
+                  float4 o = make_float4(row[q][4 * c4], row[q][4 * c4 + 1], row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
+                  if (RPT > 1) asm volatile("" : "+v"(o.x), "+v"(o.y), "+v"(o.z), "+v"(o.w));
+                  sb[1 + c4] = o;
                 }
               }
             }
           }
           __syncthreads();
           if (wact) {
-            const uint64_t pk = *kcur;
-            const int pw = (int)(pk & 15u);
             const int p = 2047 - (int)((uint32_t)pk >> 4);
             // one base register per column, the reads at immediate offsets from it (otherwise the
             // compiler forms one address per read, hoisted out of the panel loop and parked in
             // spilled registers)
-            const lds_f4* prow = lds_base(sb + pw * SLOT4 + 1);
+            const lds_f4* prow = lds_base(sb + 1);
 #pragma unroll
             for (int c4 = C0; c4 < NB4; ++c4) pr4[c4 - C0] = lds_get(prow, c4);
             const float pv = f4get<j % 4>(pr4[0]);

@@ -107,7 +107,7 @@ int set_lds(K kernel, size_t bytes) {
 
 template <bool PIVOT, int NB, int RPT, int T = kLuThreads>
 int launch_lu_nb(const LuArgs& a, int64_t batch, hipStream_t st) {
-  const size_t lds = lu_lds_bytes(a.n, NB, false, T / 64);
+  const size_t lds = lu_lds_bytes(a.n, NB);
   if (lds > kLdsMax) return RNR_ERR_UNSUPPORTED_N;
   if (int e = set_lds(k_lu<PIVOT, NB, RPT, false, T>, lds)) return e;
   k_lu<PIVOT, NB, RPT, false, T><<<dim3((unsigned)batch), dim3(T), lds, st>>>(a);
