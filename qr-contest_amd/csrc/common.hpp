@@ -38,6 +38,14 @@ __device__ __forceinline__ int xcd_remap(int pid, int total) {
   return (pid % kXcd) * per + pid / kXcd;
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16];
+// D[row][col] sits in lane col + 16 * (row / 4), register row % 4.
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 // Keeps the loads issued above this point ahead of everything below it.  Left alone, the
 // scheduler interleaves a block of independent loads with their consumers (MFMAs), so each
 // consumer waits on a load issued just before it instead of all loads sharing one latency.

@@ -47,14 +47,6 @@ struct LuArgs {
 
 constexpr int kLuThreads = 512;
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-// v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16];
-// D[row][col] sits in lane col + 16 * (row / 4), register row % 4.
-__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
 inline int lu_panel_nb(int n) { return n <= 512 ? 64 : (n <= 1024 ? 32 : 16); }
 
 // panel [n][nb+1] | -U12 chunk [nb][64] | row map [n] | pivot keys [3] (u64) | pivot row
