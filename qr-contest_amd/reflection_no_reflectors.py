@@ -48,6 +48,22 @@ def _workspace(kind: str, batch: int, n: int, device) -> torch.Tensor:
     return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
 
 
+def _check_f32_rows(A: torch.Tensor, who: str) -> int:
+    """n of a float32 (batch, n, n) CUDA tensor whose rows are contiguous; raises otherwise."""
+    if A.dim() != 3 or A.shape[-1] != A.shape[-2]:
+        raise ValueError(f"{who}: expected a (batch, n, n) tensor, got {tuple(A.shape)}")
+    if A.dtype != torch.float32:
+        raise ValueError(f"{who}: expected float32, got {A.dtype}")
+    if not A.is_cuda:
+        raise RuntimeError(f"{who}: input is on {A.device}; librnrqr runs on the GPU only")
+    n = int(A.shape[-1])
+    if n > _native.RNR_MAX_N:
+        raise ValueError(f"{who}: n = {n} exceeds the supported maximum {_native.RNR_MAX_N}")
+    if n > 0 and (A.stride(-1) != 1 or (n > 1 and A.stride(-2) != n)):
+        raise ValueError(f"{who}: rows must be contiguous with row stride n")
+    return n
+
+
 def _raise_on_info(info: torch.Tensor) -> None:
     bad = torch.nonzero(info).flatten()
     if bad.numel():
@@ -75,22 +91,25 @@ class QRPlan:
         self.info = torch.zeros(self.batch, dtype=torch.int32, device=self.device)
 
     def run(self, A: torch.Tensor, stream: int | None = None):
-        if A.dtype != torch.float32 or tuple(A.shape) != (self.batch, self.n, self.n):
-            raise ValueError("QRPlan.run: expected a float32 (batch, n, n) tensor")
-        if A.stride(-1) != 1 or A.stride(-2) != self.n:
-            raise ValueError("QRPlan.run: rows must be contiguous")
+        _check_f32_rows(A, "QRPlan.run")
+        if tuple(A.shape) != (self.batch, self.n, self.n):
+            raise ValueError(f"QRPlan.run: expected shape {(self.batch, self.n, self.n)}, got {tuple(A.shape)}")
+        if A.device != self.H.device:
+            raise ValueError(f"QRPlan.run: input is on {A.device}, the plan on {self.H.device}")
         bs = A.stride(0) if self.batch > 1 else self.n * self.n
-        st = _native.lib().rnr_qr_f32(
-            A.data_ptr(), self.batch, self.n, bs, self.H.data_ptr(), self.tau.data_ptr(),
-            self.info.data_ptr(), self.ws.data_ptr(), self.ws.numel(),
-            _stream(self.device) if stream is None else stream)
+        with torch.cuda.device(self.H.device):
+            st = _native.lib().rnr_qr_f32(
+                A.data_ptr(), self.batch, self.n, bs, self.H.data_ptr(), self.tau.data_ptr(),
+                self.info.data_ptr(), self.ws.data_ptr(), self.ws.numel(),
+                _stream(self.H.device) if stream is None else stream)
         _native.check("rnr_qr_f32", st)
         return self.H, self.tau
 
 
 def qr(A: torch.Tensor, check_errors: bool = True):
     """(H, tau) of a float32 (batch, n, n) CUDA tensor with contiguous rows."""
-    batch, n = int(A.shape[0]), int(A.shape[-1])
+    n = _check_f32_rows(A, "qr")
+    batch = int(A.shape[0])
     H = torch.empty(batch, n, n, dtype=torch.float32, device=A.device)
     tau = torch.empty(batch, n, dtype=torch.float32, device=A.device)
     if batch == 0:

@@ -156,6 +156,13 @@ def test_python_layer_rejects_cpu_and_non_square(pkg):
         pkg.custom_kernel(torch.randn(2, 8, 7))
     with pytest.raises(ValueError):
         pkg.custom_kernel(torch.randn(8))
+    # the raw float32 entry point checks dtype and device before any pointer reaches the library
+    import importlib
+    rnr = importlib.import_module("qr-contest_amd.reflection_no_reflectors")
+    with pytest.raises(ValueError, match="float32"):
+        rnr.qr(torch.randn(2, 8, 8, dtype=torch.float64))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        rnr.qr(torch.randn(2, 8, 8))
 
 
 def test_build_command_targets_gfx950_without_packed_fp32(pkg):

@@ -262,6 +262,16 @@ def test_dtype_shape_and_stride_contract(rnr):
     Hv, tv = rnr.custom_kernel(Ad.transpose(-1, -2))
     Hc, tc = rnr.custom_kernel(Ad.transpose(-1, -2).contiguous())
     assert torch.equal(Hv, Hc) and torch.equal(tv, tc)
+    # the raw float32 entry point validates its input instead of reading it wrongly
+    with pytest.raises(ValueError, match="float32"):
+        rnr.qr(Ad.double())
+    with pytest.raises(ValueError, match="contiguous"):
+        rnr.qr(Ad.transpose(-1, -2))
+    plan = rnr.QRPlan(6, 24, DEV)
+    with pytest.raises(ValueError, match="contiguous"):
+        plan.run(Ad.transpose(-1, -2))
+    Hp, tp = plan.run(Ad.transpose(-1, -2).contiguous())
+    assert torch.equal(Hp, Hc) and torch.equal(tp, tc)
     # empty batch
     He, te = rnr.custom_kernel(torch.empty(0, 8, 8, device=DEV))
     assert He.shape == (0, 8, 8) and te.shape == (0, 8)
