@@ -72,7 +72,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   const int n = a.n, i0 = ti * BM, j0 = tj * BM;
   const float* X = a.X + b * a.sx;
   const float* Y = a.Y + b * a.sy;
-  const int wi0 = (wid >> 1) * WM, wj0 = (wid & 1) * WM;
+  // On a diagonal tile the 32x32 blocks strictly below the diagonal are never used (the closure
+  // masks them; the Cholesky reads only the upper triangle of G), so only the ten upper blocks
+  // are computed, spread 3/3/2/2 over the waves when BM = 128: waves 0 and 3 take the upper
+  // three blocks of their diagonal 64x64 quadrants, waves 1 and 2 one 32-row strip each of the
+  // off-diagonal quadrant (rows 0..31 and 32..63, columns 64..127).  With BM = 64 the wave below
+  // the diagonal has nothing to do.
+  const bool diag = ti == tj;
+  int wi0 = (wid >> 1) * WM, wj0 = (wid & 1) * WM;
+  if (NB == 2 && diag && wid == 2) {  // the strip of rows 32..63, columns 64..127
+    wi0 = 32;
+    wj0 = 64;
+  }
+  // blocks this wave computes: 0 every block, 1 those with mi <= nj, 2 none, 3 the mi = 0 strip
+  const int low = !diag ? 0 : (wid == 0 || wid == 3) ? 1 : (NB == 2 ? 3 : (wid == 1 ? 0 : 2));
 
   f32x16 acc[NB][NB];
 #pragma unroll
@@ -187,34 +200,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   gload(klo);
   lstore(0, klo);
   __syncthreads();
-  for (int kc = klo; kc < n; kc += BK) {
-    const bool more = kc + BK < n;
-    if (more) gload(kc + BK);
+  auto kloop = [&](auto lowc) {
+    constexpr int LOW = decltype(lowc)::value;
+    for (int kc = klo; kc < n; kc += BK) {
+      const bool more = kc + BK < n;
+      if (more) gload(kc + BK);
+      if constexpr (LOW != 2) {
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 2) {
-      const int k = kk + h;
-      float av[NB], bv[NB];
+        for (int kk = 0; kk < BK; kk += 2) {
+          const int k = kk + h;
+          float av[NB], bv[NB];
 #pragma unroll
-      for (int mi = 0; mi < NB; ++mi) av[mi] = Xs[buf][k][wi0 + mi * 32 + l32];
+          for (int mi = 0; mi < NB; ++mi) av[mi] = Xs[buf][k][wi0 + mi * 32 + l32];
 #pragma unroll
-      for (int nj = 0; nj < NB; ++nj) bv[nj] = Ys[buf][k][wj0 + nj * 32 + l32];
+          for (int nj = 0; nj < NB; ++nj) bv[nj] = Ys[buf][k][wj0 + nj * 32 + l32];
 #pragma unroll
-      for (int mi = 0; mi < NB; ++mi)
+          for (int mi = 0; mi < NB; ++mi)
 #pragma unroll
-        for (int nj = 0; nj < NB; ++nj) acc[mi][nj] = mfma(av[mi], bv[nj], acc[mi][nj]);
+            for (int nj = 0; nj < NB; ++nj)
+              if (LOW == 0 || (LOW == 1 && mi <= nj) || (LOW == 3 && mi == 0))
+                acc[mi][nj] = mfma(av[mi], bv[nj], acc[mi][nj]);
+        }
+      }
+      if (more) lstore(buf ^ 1, kc + BK);
+      __syncthreads();
+      buf ^= 1;
     }
-    if (more) lstore(buf ^ 1, kc + BK);
-    __syncthreads();
-    buf ^= 1;
-  }
+  };
+  if (low == 0) kloop(std::integral_constant<int, 0>{});
+  else if (low == 1) kloop(std::integral_constant<int, 1>{});
+  else if (low == 3) kloop(std::integral_constant<int, 3>{});
+  else kloop(std::integral_constant<int, 2>{});
 
   float* C = a.C + b * a.sc;
   // accumulator registers 4g .. 4g + 3 hold the consecutive rows wr + 8g + 4h + (0..3): their
   // row scales are one float4 LDS read
+  const int mlim = low == 3 ? 1 : NB;  // a strip wave's other row block overlaps wave 3's blocks
 #pragma unroll
   for (int mi = 0; mi < NB; ++mi)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
+      if (mi >= mlim) continue;
       const int lr0 = wi0 + mi * 32 + 8 * g + 4 * h;
       float sc[4] = {1.f, 1.f, 1.f, 1.f};
       if constexpr (ROW_SCALE) {
