@@ -58,7 +58,7 @@ inline size_t lu_lds_bytes(int n, int nb, bool direct = false) {
 }
 
 // SPLIT = true: one launch factors only panel a.k0 and stops before its trailing update,
-// which k_lu_trail runs over many workgroups (for batches too small to fill the GPU with one
+// which k_lu_trail_g runs over many workgroups (for batches too small to fill the GPU with one
 // workgroup per matrix).  The row map then lives in a.perm between launches and L11^-1 goes
 // to a.X.
 // One wave: X = L^-1 for the 64 x 64 unit-lower L11 of a panel, written over the panel's top
@@ -630,97 +630,157 @@ __global__ __launch_bounds__(256) void k_chart_tau(const float* H, int64_t sh, f
   if (sub == 0 && c < n) tau[b * n + c] = 2.f / (acc + 1.f);
 }
 
-// Trailing update of panel a.k0 for SPLIT launches: one 256-thread workgroup per (64-column
-// chunk, 256-row group) of the trailing matrix of one matrix, the same arithmetic as k_lu's
-// fused update (each workgroup forms its chunk's -U12 itself):
-// -U12 = -(L11^-1 A12[:, chunk]) on 16x16x4 MFMA, then A22[:, chunk] += L21 (-U12) on
-// 32x32x2 MFMA in 32-row tiles, L21 staged per tile through LDS.  Rows are addressed through
-// the row map in a.perm (LU) or directly (chart).
 constexpr int kLuTrailThreads = 256;
 
 constexpr int kLuTrailRows = 256;  // rows per workgroup (eight 32-row tiles)
 
-template <bool PIVOT, int NB>
-__global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail(LuArgs a, int nchunk, int nrg) {
-  constexpr int NW = kLuTrailThreads / 64, NB4 = NB / 4;
-  __shared__ float Xs[NB][NB + 1];
-  __shared__ float U[NB][64];
-  __shared__ float Ls[NW][32][NB + 1];
+// Grouped trailing update for SPLIT launches (32-wide panels): apply the S <= 4 consecutive
+// panels starting at column kg, already factored, to the columns [cb, ce) of the rows whose
+// logical position is >= kg + 32 S:
+//
+//     U = L11^-1 A[pivot rows kg .. kg + 32 S, cb:ce]      (L11: the panels' unit-lower block)
+//     A[rows, cb:ce] -= L[rows, kg .. kg + 32 S] U
+//
+// -- the blocked LU's rank-32S update, with U formed by block forward substitution over the
+// panels (U_s = X_s (A_s - sum_{t<s} L_st U_t), X_s = L_ss^-1 from the panel launch s, slot s of
+// a.X).  The split LU calls it twice per group of four panels: before panel s is factored, to
+// bring its 32 columns up to date with panels 0 .. s-1 of the group (S = s), and after the
+// group, for everything right of it (S = 4) -- one pass over the trailing matrix per 128
+// columns instead of one per 32.  The pivot rows' own columns are read as the earlier groups
+// left them: within a group no pass writes them (U is not kept; the reference drops it).
+// One 256-thread workgroup per (64-column chunk, group of rpw rows): each forms its chunk's U
+// itself, so a workgroup takes as many rows as still leaves the GPU a few workgroups per CU
+// (the launch picks rpw), which spreads that work over more row tiles.  U is formed in LDS on
+// 16x16x4 MFMA (stored negated), each wave on its own 16 columns, so the substitution needs no
+// workgroup barrier; the row tiles run on 32x32x2 MFMA with L's rows loaded straight into
+// registers: the two half-waves take the two halves of K, so each lane's 16 S values of its row
+// are contiguous (float4 loads).
+template <bool PIVOT, int S>
+__global__ __launch_bounds__(kLuTrailThreads) void k_lu_trail_g(LuArgs a, int kg, int cb, int ce, int nchunk,
+                                                               int nrg, int rpw, int64_t xslot) {
+  constexpr int NW = kLuTrailThreads / 64, K = 32 * S, HK = K / 2;
+  __shared__ float Xs[S][32][33];
+  __shared__ __attribute__((aligned(16))) float U[K][64];  // rows 32 s + i: A_s, then -U_s
   __shared__ int pls[RNR_MAX_N];
-  const int n = a.n, k0 = a.k0, k1 = k0 + NB;
+  const int n = a.n, rb = kg + K;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int l32 = lane & 31, h = lane >> 5, l16 = lane & 15, q4 = lane >> 4;
+  const int l16 = lane & 15, q4 = lane >> 4;
   const int64_t pid = blockIdx.x;
   const int64_t b = pid / ((int64_t)nchunk * nrg);
   const int rem = (int)(pid - b * nchunk * nrg), rg = rem / nchunk;
-  const int c0 = k1 + 64 * (rem - rg * nchunk);
-  const float* cur = ((k0 == 0) ? a.src + b * a.ss : a.dst + b * a.sd);
+  const int c0 = cb + 64 * (rem - rg * nchunk);
+  const float* cur = ((kg == 0) ? a.src + b * a.ss : a.dst + b * a.sd);
   float* dst = a.dst + b * a.sd;
-  // staging loops with compile-time trip counts, so their loads issue together
 #pragma unroll
   for (int u = 0; u < RNR_MAX_N / kLuTrailThreads; ++u) {
-    const int i = k0 + tid + kLuTrailThreads * u;
+    const int i = kg + tid + kLuTrailThreads * u;
     if (i < n) pls[i] = PIVOT ? a.perm[b * n + i] : i;
   }
 #pragma unroll
-  for (int u = 0; u < NB * NB / kLuTrailThreads; ++u) {
-    const int idx = tid + kLuTrailThreads * u;
-    Xs[idx / NB][idx % NB] = a.X[b * NB * NB + idx];
+  for (int u = 0; u < S * 1024 / kLuTrailThreads; ++u) {
+    const int idx = tid + kLuTrailThreads * u, sp = idx >> 10, e = idx & 1023;
+    Xs[sp][e >> 5][e & 31] = a.X[sp * xslot + b * 1024 + e];
+  }
+  __syncthreads();
+  // the pivot rows' values of this chunk (columns past n clamped: never stored)
+#pragma unroll
+  for (int u = 0; u < K * 64 / kLuTrailThreads; ++u) {
+    const int idx = tid + kLuTrailThreads * u, i = idx >> 6, j = idx & 63;
+    U[i][j] = cur[pls[kg + i] * n + min(c0 + j, n - 1)];
   }
   __syncthreads();
 
-  // -U12 chunk: (NB/16) x 4 blocks of 16x16
-  {
-    constexpr int NJOB = (NB / 16) * 4;
-    for (int job = wid; job < NJOB; job += NW) {
-      const int bi = job >> 2, bj = job & 3;
-      const int col = c0 + bj * 16 + l16;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // block forward substitution, wave w on the chunk's columns 16 w .. 16 w + 15, both 16-row
+  // halves of each 32-row block (D[i][j] of a 16x16x4 result: lane j + 16 (i / 4), register i % 4)
+  const int wc = 16 * wid + l16;
 #pragma unroll
-      for (int t = 0; t < NB4; ++t) {
-        const int k = 4 * t + q4;
-        const float bv = cur[pls[k0 + k] * n + min(col, n - 1)];  // columns past n: not stored
-        acc = mfma16(Xs[bi * 16 + l16][k], bv, acc);
+  for (int sp = 0; sp < S; ++sp) {
+    f32x4 acc[2];
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[ti][r] = U[32 * sp + 16 * ti + 4 * q4 + r][wc];
+    // T = A_s + sum_{t < s} L_st (-U_t)
+#pragma unroll
+    for (int t = 0; t < sp; ++t) {
+      float av[2][8];
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti) {
+        const float* lr = dst + pls[kg + 32 * sp + 16 * ti + l16] * n + kg + 32 * t + q4;
+#pragma unroll
+        for (int k4 = 0; k4 < 8; ++k4) av[ti][k4] = lr[4 * k4];
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) U[bi * 16 + 4 * q4 + r][bj * 16 + l16] = -acc[r];
+      for (int k4 = 0; k4 < 8; ++k4) {
+        const float bv = U[32 * t + 4 * k4 + q4][wc];
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti) acc[ti] = mfma16(av[ti][k4], bv, acc[ti]);
+      }
     }
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) U[32 * sp + 16 * ti + 4 * q4 + r][wc] = acc[ti][r];
+    wave_lds_order();
+    // -U_s = -X_s T, over T in place (the wave's own columns: every read precedes the stores)
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) acc[ti] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k4 = 0; k4 < 8; ++k4) {
+      const float bv = U[32 * sp + 4 * k4 + q4][wc];
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti) acc[ti] = mfma16(Xs[sp][16 * ti + l16][4 * k4 + q4], bv, acc[ti]);
+    }
+    wave_lds_order();
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) U[32 * sp + 16 * ti + 4 * q4 + r][wc] = -acc[ti][r];
+    wave_lds_order();
   }
   __syncthreads();
 
-  const int ntr = min((n - k1 + 31) >> 5, (rg + 1) * (kLuTrailRows / 32));
-  for (int tr = rg * (kLuTrailRows / 32) + wid; tr < ntr; tr += NW) {
-    const int r0 = k1 + tr * 32;
-    // L21 rows r0 .. r0 + 31 (columns k0 .. k1) into this wave's tile (unrolled: the loads
-    // issue together)
+  // the row tiles: C[32 x 64] += L[32 x K] (-U)[K x 64], half-wave h on k in [h K/2, (h+1) K/2)
+  const int tpw = rpw >> 5;  // row tiles per workgroup
+  const int ntr = min((n - rb + 31) >> 5, (rg + 1) * tpw);
+  for (int tr = rg * tpw + wid; tr < ntr; tr += NW) {
+    const int r0 = rb + tr * 32;
+    int ln = lane;  // laundered per tile: the row offsets are formed here, not kept live
+    asm volatile("" : "+v"(ln));
+    const int l32 = ln & 31, h = ln >> 5;
+    const float* lrow = dst + pls[min(r0 + l32, n - 1)] * n + kg + h * HK;  // rows past n clamped: never stored
+    float lv[HK];
+    if (a.vec4) {
 #pragma unroll
-    for (int idx = lane; idx < 32 * NB; idx += 64) {  // rows past n clamped: never stored
-      const int rr = idx / NB, k = idx - rr * NB, rw = min(r0 + rr, n - 1);
-      Ls[wid][rr][k] = dst[pls[rw] * n + k0 + k];
+      for (int u = 0; u < HK / 4; ++u) {
+        const float4 v = *reinterpret_cast<const float4*>(lrow + 4 * u);
+        lv[4 * u] = v.x; lv[4 * u + 1] = v.y; lv[4 * u + 2] = v.z; lv[4 * u + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < HK; ++t) lv[t] = lrow[t];
     }
-    wave_lds_order();
     f32x16 c[2];
 #pragma unroll
     for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int rw = min(r0 + acc_row(r, lane), n - 1), col = min(c0 + nj * 32 + l32, n - 1);
+        const int rw = min(r0 + acc_row(r, ln), n - 1), col = min(c0 + nj * 32 + l32, n - 1);
         c[nj][r] = cur[pls[rw] * n + col];  // clamped rows / columns are not stored
       }
+    issue_loads_first();
 #pragma unroll
-    for (int kk = 0; kk < NB; kk += 2) {
-      const int k = kk + h;
-      const float av = Ls[wid][l32][k];
-      c[0] = mfma(av, U[k][l32], c[0]);
-      c[1] = mfma(av, U[k][32 + l32], c[1]);
+    for (int t = 0; t < HK; ++t) {
+      const int k = h * HK + t;
+      c[0] = mfma(lv[t], U[k][l32], c[0]);
+      c[1] = mfma(lv[t], U[k][32 + l32], c[1]);
     }
-    wave_lds_order();  // the next tile's L21 stores stay behind these reads
 #pragma unroll
     for (int nj = 0; nj < 2; ++nj)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int rw = r0 + acc_row(r, lane), col = c0 + nj * 32 + l32;
-        if (rw < n && col < n) dst[pls[rw] * n + col] = c[nj][r];
+        const int rw = r0 + acc_row(r, ln), col = c0 + nj * 32 + l32;
+        if (rw < n && col < ce) dst[pls[rw] * n + col] = c[nj][r];
       }
   }
 }

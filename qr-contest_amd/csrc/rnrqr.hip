@@ -115,32 +115,64 @@ int launch_lu_nb(const LuArgs& a, int64_t batch, hipStream_t st) {
 }
 
 // Batches too small to occupy the GPU with one workgroup per matrix (fewer matrices than
-// half the CUs) at n > 512: each LU / chart panel is its own launch, and its trailing update is
-// spread over one workgroup per 64-column chunk (k_lu_trail); the Cholesky likewise runs per
-// block (k_chol_diag / k_chol_row / k_chol_trail).
+// half the CUs) at n > 512: each LU / chart panel is its own launch, and the trailing updates
+// are spread over one workgroup per 64-column chunk (k_lu_trail_g, once per group of four
+// panels); the Cholesky likewise runs per block (k_chol_diag / k_chol_row / k_chol_trail).
 bool lu_split(int64_t batch, int n) { return n > 512 && batch < 128; }
 
-template <bool PIVOT, int NB, int RPT>
+// Grouped update: panels kg .. kg + 32 S applied to columns [cb, ce) of the rows below them.
+template <bool PIVOT>
+void launch_lu_trail_g(const LuArgs& a, int S, int kg, int cb, int ce, int64_t batch, hipStream_t st) {
+  const int rb = kg + 32 * S, rows = a.n - rb;
+  const int nchunk = (ce - cb + 63) / 64;
+  // rows per workgroup: each workgroup forms its chunk's U itself, so it takes as many rows as
+  // still leaves about 2 workgroups per CU (at least 256)
+  int rpw = kLuTrailRows;
+  while (rpw < rows && batch * nchunk * ((rows + 2 * rpw - 1) / (2 * rpw)) >= 512) rpw *= 2;
+  const int nrg = (rows + rpw - 1) / rpw;
+  const dim3 grid((unsigned)(batch * nchunk * nrg)), block(kLuTrailThreads);
+  const int64_t xslot = batch * 1024;
+  switch (S) {
+    case 1: k_lu_trail_g<PIVOT, 1><<<grid, block, 0, st>>>(a, kg, cb, ce, nchunk, nrg, rpw, xslot); break;
+    case 2: k_lu_trail_g<PIVOT, 2><<<grid, block, 0, st>>>(a, kg, cb, ce, nchunk, nrg, rpw, xslot); break;
+    case 3: k_lu_trail_g<PIVOT, 3><<<grid, block, 0, st>>>(a, kg, cb, ce, nchunk, nrg, rpw, xslot); break;
+    default: k_lu_trail_g<PIVOT, 4><<<grid, block, 0, st>>>(a, kg, cb, ce, nchunk, nrg, rpw, xslot); break;
+  }
+}
+
+// 32-wide panels in groups of four: panel s of a group is first brought up to date with the
+// group's earlier panels (its 32 columns only), then factored (L11^-1 to slot s of the xbuf);
+// after the group one rank-128 pass updates everything right of it.
+template <bool PIVOT, int RPT>
 int launch_lu_split(LuArgs a, int64_t batch, hipStream_t st) {
-  const size_t lds = lu_lds_bytes(a.n, NB, NB == 32);  // 32-wide split panels keep only L11 in LDS
+  constexpr int NB = 32, G = 4;
+  const size_t lds = lu_lds_bytes(a.n, NB, true);  // the panel's rows stay out of LDS (L11 only)
   if (lds > kLdsMax) return RNR_ERR_UNSUPPORTED_N;
   if (int e = set_lds(k_lu<PIVOT, NB, RPT, true>, lds)) return e;
-  for (int k0 = 0; k0 < a.n; k0 += NB) {
-    a.k0 = k0;
-    k_lu<PIVOT, NB, RPT, true><<<dim3((unsigned)batch), dim3(kLuThreads), lds, st>>>(a);
-    const int k1 = k0 + NB;
-    if (k1 >= a.n) break;
-    const int nchunk = (a.n - k1 + 63) / 64, nrg = (a.n - k1 + kLuTrailRows - 1) / kLuTrailRows;
-    k_lu_trail<PIVOT, NB><<<dim3((unsigned)(batch * nchunk * nrg)), dim3(kLuTrailThreads), 0, st>>>(a, nchunk, nrg);
+  const int n = a.n;
+  float* const xbase = a.X;
+  for (int kg = 0; kg < n; kg += G * NB) {
+    const int np = min(G, (n - kg + NB - 1) / NB);  // panels in this group
+    for (int sp = 0; sp < np; ++sp) {
+      const int kp = kg + NB * sp;
+      a.X = xbase;
+      if (sp > 0) launch_lu_trail_g<PIVOT>(a, sp, kg, kp, min(kp + NB, n), batch, st);
+      a.k0 = kp;
+      a.X = xbase + (int64_t)sp * batch * NB * NB;
+      k_lu<PIVOT, NB, RPT, true><<<dim3((unsigned)batch), dim3(kLuThreads), lds, st>>>(a);
+    }
+    a.X = xbase;
+    if (kg + G * NB < n) launch_lu_trail_g<PIVOT>(a, G, kg, kg + G * NB, n, batch, st);
   }
-  if (!PIVOT && NB == 32) {  // the chart's tau, from the finished multipliers
-    const int ncb = (a.n + 31) / 32;
-    k_chart_tau<<<dim3((unsigned)(batch * ncb)), dim3(256), 0, st>>>(a.dst, a.sd, a.tau, a.n, ncb);
+  if (!PIVOT) {  // the chart's tau, from the finished multipliers
+    const int ncb = (n + 31) / 32;
+    k_chart_tau<<<dim3((unsigned)(batch * ncb)), dim3(256), 0, st>>>(a.dst, a.sd, a.tau, n, ncb);
   }
   return hip_status();
 }
 
-// xbuf: [batch][64][64] floats of scratch for the split form (L11^-1 between launches).
+// xbuf: batch * 64 * 64 floats of scratch for the split form (the four 32x32 L11^-1 of a panel
+// group between launches, slot-major).
 int launch_lu(bool pivot, const float* src, int64_t ss, float* dst, int64_t sd, int64_t batch,
               int n, int* perm, float* L, float* s, float* tau, float* xbuf, hipStream_t st) {
   LuArgs a;
@@ -152,8 +184,8 @@ int launch_lu(bool pivot, const float* src, int64_t ss, float* dst, int64_t sd, 
   if (lu_split(batch, n) && xbuf) {
     // 32-wide panels at every split size: the panel's rows go straight between HBM and registers,
     // so its width is not bound by an n-row LDS copy (rank-32 trailing updates, half the passes)
-    if (pivot) return n <= 1024 ? launch_lu_split<true, 32, 2>(a, batch, st) : launch_lu_split<true, 32, 4>(a, batch, st);
-    return n <= 1024 ? launch_lu_split<false, 32, 2>(a, batch, st) : launch_lu_split<false, 32, 4>(a, batch, st);
+    if (pivot) return n <= 1024 ? launch_lu_split<true, 2>(a, batch, st) : launch_lu_split<true, 4>(a, batch, st);
+    return n <= 1024 ? launch_lu_split<false, 2>(a, batch, st) : launch_lu_split<false, 4>(a, batch, st);
   }
   // rows per thread: n <= T * RPT; one row per thread with 128 or 256 threads at n <= 128 / 256
   if (pivot) {
