@@ -58,7 +58,7 @@ def stage_symbols(batch: int, n: int) -> dict:
         rpt = 2 if n <= 1024 else 4
         lu = f"rnr::k_lu<true, 32, {rpt}, true, 512> + rnr::k_lu_trail_g<true, 1..4>"
         chart = f"rnr::k_lu<false, 32, {rpt}, true, 512> + rnr::k_lu_trail_g<false, 1..4> + rnr::k_chart_tau"
-        chol = "rnr::k_chol_jitter + rnr::k_chol_diag + rnr::k_chol_row + rnr::k_chol_trail"
+        chol = "rnr::k_chol_jitter + rnr::k_chol_diag + rnr::k_chol_row + rnr::k_chol_step"
     else:
         nb, rpt = (64, 1) if n <= 512 else ((32, 2) if n <= 1024 else (16, 4))
         t = 128 if n <= 128 else (256 if n <= 256 else 512)  # workgroup size (launch_lu)

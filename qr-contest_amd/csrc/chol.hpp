@@ -435,6 +435,7 @@ struct CholSplitArgs {
   float* Dinv;
   int* info;
   int n, k0, keep_info, njob;
+  int nb;  // k_chol_step: the batch (its first nb workgroups factor the next diagonal block)
 };
 
 __global__ __launch_bounds__(kCholThreads) void k_chol_jitter(CholSplitArgs a) {
@@ -456,25 +457,13 @@ __global__ __launch_bounds__(kCholThreads) void k_chol_jitter(CholSplitArgs a) {
   if (tid == 0 && (!a.keep_info || a.info[b] == 0)) a.info[b] = 0;
 }
 
-__global__ __launch_bounds__(64) void k_chol_diag(CholSplitArgs a) {
-  __shared__ float D[64 * 65];
-  __shared__ __attribute__((aligned(16))) float XT[64 * 68];  // RT while factoring, then XT
-  __shared__ float RI[64];
-  __shared__ __attribute__((aligned(16))) float SB[128];
-  const int n = a.n, k0 = a.k0, b = blockIdx.x, lane = threadIdx.x;
-  const int kb = min(kCholNb, n - k0);
+// Wave 0 of a split-form launch: factor and invert the diagonal block at k0 held in D (upper
+// part; the identity past n), write R_kk (upper) and Dinv_kk, record a failed pivot in info.
+__device__ __forceinline__ void chol_split_factor(const CholSplitArgs& a, int b, int k0, float* D, float* XT,
+                                                  float* RI, float* SB, int lane) {
+  const int n = a.n, kb = min(kCholNb, n - k0);
   float* G = a.G + b * a.sg;
   float* Dv = a.Dinv + (int64_t)b * n * 64;
-  {
-    // the block row by row, the lanes along each row: all 64 loads in flight together
-    // (addresses clamped past n, the identity written there)
-    const int cl = min(lane, kb - 1);
-    float v[64];
-#pragma unroll
-    for (int i = 0; i < 64; ++i) v[i] = G[(k0 + min(i, kb - 1)) * n + k0 + cl];
-#pragma unroll
-    for (int i = 0; i < 64; ++i) D[i * 65 + lane] = (i < kb && lane < kb) ? v[i] : (i == lane ? 1.f : 0.f);
-  }
   wave_lds_order();
   const int fail = chol_diag_wave(D, XT, RI, SB, lane);
   if (lane == 0 && fail != INT_MAX && fail < kb && a.info[b] == 0) a.info[b] = k0 + fail + 1;
@@ -487,6 +476,27 @@ __global__ __launch_bounds__(64) void k_chol_diag(CholSplitArgs a) {
     if (c < kb && c >= i) G[(k0 + i) * n + k0 + c] = D[i * 65 + c];
     Dv[(k0 + i) * 64 + c] = (c < kb) ? XT[c * 65 + i] : 0.f;
   }
+}
+
+__global__ __launch_bounds__(64) void k_chol_diag(CholSplitArgs a) {
+  __shared__ float D[64 * 65];
+  __shared__ __attribute__((aligned(16))) float XT[64 * 68];  // RT while factoring, then XT
+  __shared__ float RI[64];
+  __shared__ __attribute__((aligned(16))) float SB[128];
+  const int n = a.n, k0 = a.k0, b = blockIdx.x, lane = threadIdx.x;
+  const int kb = min(kCholNb, n - k0);
+  const float* G = a.G + b * a.sg;
+  {
+    // the block row by row, the lanes along each row: all 64 loads in flight together
+    // (addresses clamped past n, the identity written there)
+    const int cl = min(lane, kb - 1);
+    float v[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) v[i] = G[(k0 + min(i, kb - 1)) * n + k0 + cl];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) D[i * 65 + lane] = (i < kb && lane < kb) ? v[i] : (i == lane ? 1.f : 0.f);
+  }
+  chol_split_factor(a, b, k0, D, XT, RI, SB, lane);
 }
 
 // R_k,> = Dinv_kk^T G_k,>: wave w of workgroup g takes the 32 columns starting at
@@ -539,15 +549,11 @@ __global__ __launch_bounds__(kCholSplitThreads) void k_chol_row(CholSplitArgs a)
   }
 }
 
-// G_>,> -= R_k,>^T R_k,>: wave w of workgroup g takes upper tile pair 4 g + w.
-__global__ __launch_bounds__(kCholSplitThreads) void k_chol_trail(CholSplitArgs a) {
+// One upper 64x64 tile pair pr of G_>,> -= R_k,>^T R_k,> (the trailing matrix right of block k0).
+__device__ __forceinline__ void chol_trail_pair(const CholSplitArgs& a, int64_t b, int pr, int lane) {
   const int n = a.n, k0 = a.k0, k1 = k0 + kCholNb, w = n - k1;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, l32 = lane & 31, h = lane >> 5;
-  const int nt = (w + 63) >> 6, npairs = nt * (nt + 1) / 2;
-  const int64_t pid = blockIdx.x;
-  const int64_t b = pid / a.njob;
-  const int pr = 4 * (int)(pid - b * a.njob) + wid;
-  if (pr >= npairs) return;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int nt = (w + 63) >> 6;
   float* G = a.G + b * a.sg;
   int I, J;
   upper_tile(pr, nt, I, J);
@@ -584,5 +590,58 @@ __global__ __launch_bounds__(kCholSplitThreads) void k_chol_trail(CholSplitArgs 
         if (row < n && col < n) G[row * n + col] = acc[mi][nj][r];
       }
 }
+
+// The trailing update of block k0 and the factor of the next diagonal block, in one launch so
+// the two run side by side.  Workgroups [0, batch) take matrix b's next diagonal tile (tile pair
+// 0): its upper 32x32 quadrants updated by the block row on waves 0-2 straight into LDS (the
+// lower-left one is never read by the factor), then wave 0 factors and inverts it as
+// k_chol_diag does.  The others take tile pairs 1 .. npairs - 1, one per wave (a.njob
+// workgroups per matrix).
+__global__ __launch_bounds__(kCholSplitThreads) void k_chol_step(CholSplitArgs a) {
+  __shared__ float D[64 * 65];
+  __shared__ __attribute__((aligned(16))) float XT[64 * 68];  // RT while factoring, then XT
+  __shared__ float RI[64];
+  __shared__ __attribute__((aligned(16))) float SB[128];
+  const int n = a.n, k0 = a.k0, k1 = k0 + kCholNb, w = n - k1;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t pid = blockIdx.x;
+  if (pid < a.nb) {
+    const int b = (int)pid, kbn = min(kCholNb, w);
+    const float* G = a.G + b * a.sg;
+    if (wid < 3) {
+      const int qi = wid == 2 ? 1 : 0, qj = wid == 0 ? 0 : 1;
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int l32 = ln & 31, h = ln >> 5;
+      f32x16 q;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {  // rows / columns past n clamped: never stored
+        const int row = min(k1 + 32 * qi + acc_row(r, ln), n - 1);
+        const int col = min(k1 + 32 * qj + l32, n - 1);
+        q[r] = G[row * n + col];
+      }
+      issue_loads_first();
+      const int ci = 32 * qi + l32, cj = 32 * qj + l32;
+#pragma unroll 8
+      for (int kk = 0; kk < kCholNb; kk += 2) {
+        const float* gk = G + (k0 + kk + h) * n + k1;
+        q = mfma(-gk[ci], gk[cj], q);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = 32 * qi + acc_row(r, ln), c = 32 * qj + l32;
+        D[i * 65 + c] = (i < kbn && c < kbn) ? q[r] : (i == c ? 1.f : 0.f);
+      }
+    }
+    __syncthreads();
+    if (wid == 0) chol_split_factor(a, b, k1, D, XT, RI, SB, lane);
+    return;
+  }
+  const int64_t q = pid - a.nb, b = q / a.njob;
+  const int nt = (w + 63) >> 6, npairs = nt * (nt + 1) / 2;
+  const int pr = 1 + 4 * (int)(q - b * a.njob) + wid;
+  if (pr < npairs) chol_trail_pair(a, b, pr, lane);
+}
+
 
 }  // namespace rnr

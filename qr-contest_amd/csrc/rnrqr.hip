@@ -6,7 +6,7 @@
 //   3. k_chol            G -> R_a (upper, jittered), Dinv, info                 (:74-76)
 //      k_wblocks         W = off-diagonal blocks of R_a times Dinv -> Qb (the solve's operand)
 //                        (n > 512 with fewer than 128 matrices: k_chol_jitter, then per
-//                        64-column block k_chol_diag / k_chol_row / k_chol_trail instead of k_chol)
+//                        64-column block k_chol_row / k_chol_step after a first k_chol_diag instead of k_chol)
 //   4. k_trsm            Q1 = L R_a^-1 -> L buffer                              (:77)
 //   5. k_tn_upper        G = Q1^T Q1                                            (:73)
 //   6. k_chol            G -> R_b, Dinv, info                                   (:74-76)
@@ -117,7 +117,8 @@ int launch_lu_nb(const LuArgs& a, int64_t batch, hipStream_t st) {
 // Batches too small to occupy the GPU with one workgroup per matrix (fewer matrices than
 // half the CUs) at n > 512: each LU / chart panel is its own launch, and the trailing updates
 // are spread over one workgroup per 64-column chunk (k_lu_trail_g, once per group of four
-// panels); the Cholesky likewise runs per block (k_chol_diag / k_chol_row / k_chol_trail).
+// panels); the Cholesky likewise runs per block (k_chol_row, then k_chol_step: trailing tiles
+// beside the next diagonal factor).
 bool lu_split(int64_t batch, int n) { return n > 512 && batch < 128; }
 
 // Grouped update: panels kg .. kg + 32 S applied to columns [cb, ce) of the rows below them.
@@ -265,18 +266,21 @@ int launch_chol(float* G, int64_t sg, float* Dinv, int* info, int64_t batch, int
   if (lu_split(batch, n)) {
     // small batch: per 64-column block a diagonal launch (one wave per matrix), then the
     // block row and the trailing tiles spread over one wave per 32 columns / per tile
-    CholSplitArgs c{G, sg, Dinv, info, n, 0, a.keep_info, 0};
+    // small batch: the first diagonal block, then per 64-column block the block row (one wave
+    // per 32 columns) and one launch that runs the trailing tiles (one wave per tile) beside the
+    // next diagonal block's update and factor (one workgroup per matrix)
+    CholSplitArgs c{G, sg, Dinv, info, n, 0, a.keep_info, 0, (int)batch};
     k_chol_jitter<<<dim3((unsigned)batch), dim3(kCholThreads), 0, st>>>(c);
+    k_chol_diag<<<dim3((unsigned)batch), dim3(64), 0, st>>>(c);
     for (int k0 = 0; k0 < n; k0 += kCholNb) {
-      c.k0 = k0;
-      k_chol_diag<<<dim3((unsigned)batch), dim3(64), 0, st>>>(c);
       const int w = n - k0 - kCholNb;
       if (w <= 0) break;
+      c.k0 = k0;
       c.njob = (w + 127) / 128;
       k_chol_row<<<dim3((unsigned)(batch * c.njob)), dim3(kCholSplitThreads), 0, st>>>(c);
       const int nt = (w + 63) / 64;
-      c.njob = (nt * (nt + 1) / 2 + 3) / 4;
-      k_chol_trail<<<dim3((unsigned)(batch * c.njob)), dim3(kCholSplitThreads), 0, st>>>(c);
+      c.njob = (nt * (nt + 1) / 2 - 1 + 3) / 4;  // tile pairs 1 .. npairs - 1
+      k_chol_step<<<dim3((unsigned)(batch * (1 + c.njob))), dim3(kCholSplitThreads), 0, st>>>(c);
     }
   } else {
     a.strip_lds = chol_lds_bytes(n, true) <= kLdsMax ? 1 : 0;
