@@ -79,8 +79,9 @@ def stage_symbols(batch: int, n: int) -> dict:
 
     rb = 64 if batch * ((n + 127) // 128) < 512 else 128
     trsm = f"rnr::k_trsm<{tf(vec4)}, {rb}>"
-    return {"lu": lu, "gram_L": tn(False, True), "chol_1": chol, "wblk_1": "rnr::k_wblocks", "trsm_1": trsm,
-            "gram_Q1": tn(False, False), "chol_2": chol, "wblk_2": "rnr::k_wblocks", "trsm_2": trsm,
+    wblk = "rnr::k_wblocks" if split else chol  # the fused Cholesky forms the W blocks itself
+    return {"lu": lu, "gram_L": tn(False, True), "chol_1": chol, "wblk_1": wblk, "trsm_1": trsm,
+            "gram_Q1": tn(False, False), "chol_2": chol, "wblk_2": wblk, "trsm_2": trsm,
             "chart": chart, "closure": tn(True, False)}
 
 

@@ -31,6 +31,8 @@ struct CholArgs {
   int n;
   int strip_lds;
   int keep_info;  // 1: leave an earlier non-zero info in place
+  float* Wm;      // non-null: also form the solve's operand -W[k][c] = -R[k][c] Dinv_c (k < c) here,
+  int64_t sw;     // at the R positions of a [batch][n][n] buffer (batch stride sw)
 };
 
 constexpr int kCholThreads = 512;
@@ -231,6 +233,42 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_c
 
   // Iteration k0 = -64 has no block of its own: its "trailing update" is wave 0 taking the
   // first diagonal block from G (so the factor and the inverse exist once in the code).
+  // -W[:k, k] = -R[:k, k] Dinv_kk for block k at k0 (kb columns), strip m = rows 32 m .. + 31:
+  // A = R[row][k0 + kk] (lane: row l32, kk = 2 t + h), B = Dinv_kk[kk][j] -- from its transposed
+  // LDS copy XT, or (while the next factor overwrites XT) from HBM.  Columns of the block past n
+  // meet zero rows of Dinv.
+  auto w_strip = [&](int m, int k0, int kb, bool lds) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int l32 = ln & 31, h = ln >> 5;
+    const float* rr = G + (32 * m + l32) * n;
+    float av[32];
+#pragma unroll
+    for (int t = 0; t < 32; ++t) av[t] = rr[min(k0 + 2 * t + h, n - 1)];
+    float* W = a.Wm + b * a.sw;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int j = 32 * half + l32;
+      f32x16 acc = zero16();
+      if (lds) {
+        issue_loads_first();
+#pragma unroll
+        for (int t = 0; t < 32; ++t) acc = mfma(av[t], XT[j * 65 + 2 * t + h], acc);
+      } else {
+        float bw[32];
+#pragma unroll
+        for (int t = 0; t < 32; ++t) bw[t] = Dv[(k0 + 2 * t + h) * 64 + j];
+        issue_loads_first();
+#pragma unroll
+        for (int t = 0; t < 32; ++t) acc = mfma(av[t], bw[t], acc);
+      }
+      if (j < kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) W[(32 * m + acc_row(r, ln)) * n + k0 + j] = -acc[r];
+      }
+    }
+  };
+
   for (int k0 = -kCholNb; k0 < n; k0 += kCholNb) {
     const bool first = k0 < 0;
     const int kb = first ? 0 : min(kCholNb, n - k0), k1 = first ? 0 : k0 + kb, w = n - k1;
@@ -242,12 +280,15 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_c
         if (c < kb && c >= i) G[(k0 + i) * n + k0 + c] = D[i * 65 + c];
         Dv[(k0 + i) * 64 + c] = (c < kb) ? XT[c * 65 + i] : 0.f;
       }
-      if (w <= 0) break;  // uniform; kb == 64 below this line
-
       // block row R_k,> = Dinv_kk^T G_k,>: each wave owns 32 columns (both 32-row halves),
-      // so it can overwrite them in G without racing other waves' reads.
-      const int nch = (w + 31) >> 5;
-      for (int job = wid; job < nch; job += NW) {
+      // so it can overwrite them in G without racing other waves' reads.  After the last
+      // block (no trailing phase) the same loop forms that block's W strips (see w_strip).
+      const int nch = w > 0 ? (w + 31) >> 5 : 0, nwj = (a.Wm && w <= 0) ? k0 >> 5 : 0;
+      for (int job = wid; job < nch + nwj; job += NW) {
+        if (job >= nch) {
+          w_strip(job - nch, k0, kb, true);
+          continue;
+        }
         // lane-derived offsets are laundered per job: hoisted out of the block loop they
         // would stay live across it (32+ VGPRs) and spill
         int ln = lane;
@@ -279,6 +320,7 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_c
           }
         }
       }
+      if (w <= 0) break;  // uniform; kb == 64 below this line
       __syncthreads();
     }
 
@@ -412,6 +454,10 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_c
               }
         }
       }
+      // this block's W strips on the waves past their tiles (wave 0's factor is the longer
+      // chain); Dinv_kk went to HBM before the block row's barrier
+      if (!first && a.Wm && wid > 0)
+        for (int m = wid - 1; m < (k0 >> 5); m += NW - 1) w_strip(m, k0, kb, false);
     }
     __syncthreads();
   }

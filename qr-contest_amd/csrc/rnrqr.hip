@@ -3,14 +3,13 @@
 // Launch sequence of rnr_qr_f32 on the caller's stream (reflection_no_reflectors.py:181-196):
 //   1. k_lu<true>        A -> W (in-place factor, A's row order), perm, L      (:66)
 //   2. k_tn_upper        G = L^T L, upper tiles, zero rows of L skipped         (:73)
-//   3. k_chol            G -> R_a (upper, jittered), Dinv, info                 (:74-76)
-//      k_wblocks         W = off-diagonal blocks of R_a times Dinv -> Qb (the solve's operand)
-//                        (n > 512 with fewer than 128 matrices: k_chol_jitter, then per
-//                        64-column block k_chol_row / k_chol_step after a first k_chol_diag instead of k_chol)
+//   3. k_chol            G -> R_a (upper, jittered), Dinv, info, and W = the off-diagonal
+//                        blocks of R_a times Dinv -> Qb (the solve's operand)      (:74-76)
+//                        (n > 512 with fewer than 128 matrices: k_chol_jitter, k_chol_diag, then
+//                        per 64-column block k_chol_row / k_chol_step, and W from k_wblocks)
 //   4. k_trsm            Q1 = L R_a^-1 -> L buffer                              (:77)
 //   5. k_tn_upper        G = Q1^T Q1                                            (:73)
-//   6. k_chol            G -> R_b, Dinv, info                                   (:74-76)
-//      k_wblocks         W for R_b -> the (now dead) LU buffer
+//   6. k_chol            G -> R_b, Dinv, info; W for R_b -> the (now dead) LU buffer (:74-76)
 //   7. k_trsm            Q = P (Q1 R_b^-1) -> Qb (row scatter)                   (:77,81)
 //   8. k_lu<false>       chart of Q, read from Qb, worked in H: tails Y, signs  (:139-174,192)
 //                        s, tau (Qb stays intact for the closure)
@@ -258,11 +257,14 @@ int launch_wblocks(const float* R, int64_t sr, const float* Dinv, float* Wm, int
   return hip_status();
 }
 
+// Wm non-null: the one-workgroup-per-matrix Cholesky also forms the solve's W blocks there
+// (the split form leaves them to k_wblocks).
 int launch_chol(float* G, int64_t sg, float* Dinv, int* info, int64_t batch, int n, bool keep_info,
-                hipStream_t st) {
+                float* Wm, hipStream_t st) {
   CholArgs a;
   a.G = G; a.sg = sg; a.Dinv = Dinv; a.info = info; a.n = n;
   a.keep_info = keep_info ? 1 : 0;
+  a.Wm = Wm; a.sw = (int64_t)n * n;
   if (lu_split(batch, n)) {
     // small batch: per 64-column block a diagonal launch (one wave per matrix), then the
     // block row and the trailing tiles spread over one wave per 32 columns / per tile
@@ -360,9 +362,11 @@ int cholqr_pass(const float* M, int64_t sm, const int* lperm, float* G, float* D
   if (int e = launch_tn(false, M, sm, M, sm, G, nn, nullptr, lperm, batch, n, lperm != nullptr, st))
     return e;
   if (int e = mk.mark(st)) return e;
-  if (int e = launch_chol(G, nn, Dinv, info, batch, n, keep_info, st)) return e;
+  const bool w_in_chol = !lu_split(batch, n);  // the fused Cholesky forms W itself
+  if (int e = launch_chol(G, nn, Dinv, info, batch, n, keep_info, w_in_chol ? Wm : nullptr, st)) return e;
   if (int e = mk.mark(st)) return e;
-  if (int e = launch_wblocks(G, nn, Dinv, Wm, batch, n, st)) return e;
+  if (!w_in_chol)
+    if (int e = launch_wblocks(G, nn, Dinv, Wm, batch, n, st)) return e;
   if (int e = mk.mark(st)) return e;
   return launch_trsm(M, sm, lperm, Wm, nn, Dinv, Q, nn, Q2, nn, perm, batch, n, st);
 }
