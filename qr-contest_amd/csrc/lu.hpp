@@ -285,21 +285,19 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_l
           // their full wave width whatever the active lanes, so one wave storing beats every
           // wave storing its own candidate
           const uint64_t pk = *kcur;
-          if (wact && best == pk) {
-            // one masked store block per row of the thread, only the winner's executing (the
-            // stored values pass through an empty asm so the blocks are not merged into a
-            // lane-dependent index into row[], which would put row[] on the stack)
+          const bool winner = wact && best == pk;
+          // one masked store block per row of the thread, only the winner's executing; a
+          // compiler memory barrier between the blocks keeps them apart (merged, they would
+          // become copies into common registers, or a lane-dependent index into row[] that puts
+          // row[] on the stack)
 #pragma unroll
-            for (int q = 0; q < RPT; ++q) {
-              if (RPT == 1 || bq == q) {
+          for (int q = 0; q < RPT; ++q) {
+            if (winner && (RPT == 1 || bq == q)) {
 #pragma unroll
-                for (int c4 = C0; c4 < NB4; ++c4) {
-                  float4 o = make_float4(row[q][4 * c4], row[q][4 * c4 + 1], row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
-                  if (RPT > 1) asm volatile("" : "+v"(o.x), "+v"(o.y), "+v"(o.z), "+v"(o.w));
-                  sb[1 + c4] = o;
-                }
-              }
+              for (int c4 = C0; c4 < NB4; ++c4)
+                sb[1 + c4] = make_float4(row[q][4 * c4], row[q][4 * c4 + 1], row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
             }
+            if (RPT > 1) asm volatile("" ::: "memory");
           }
           __syncthreads();
           if (wact) {
