@@ -137,6 +137,27 @@ __device__ __forceinline__ void rank1_from_slot(float (&x)[NP], float l, const f
   }
 }
 
+// Broadcast within each group of NP lanes from the group's lane p[g] (uniform lane indices, one
+// per group): readlane into scalar registers, no LDS (whose instructions cost their full width
+// even for one storing lane, on a pipe every wave of the CU shares).  For 1 or 2 groups per wave.
+template <int G>
+__device__ __forceinline__ float group_bcast(float v, const int (&p)[G], bool upper) {
+  const float u0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), p[0]));
+  if constexpr (G == 1) {
+    return u0;
+  } else {
+    const float u1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), p[1]));
+    return upper ? u1 : u0;
+  }
+}
+
+// x[c] -= l * (x[c] of the group's lane p) for compile-time c > J
+template <int NP, int G, int J>
+__device__ __forceinline__ void rank1_from_lanes(float (&x)[NP], float l, const int (&p)[G], bool upper) {
+#pragma unroll
+  for (int c = J + 1; c < NP; ++c) x[c] -= l * group_bcast<G>(x[c], p, upper);
+}
+
 // acc[g][u] = upper 16x16 blocks (bi <= bj, row-major order u) of X_g^T Y_g for the G
 // matrices of this wave: X_g, Y_g are NP x NP (row stride LD) at X + g*MAT, Y + g*MAT,
 // zero past row and column n.
@@ -175,7 +196,8 @@ __device__ __forceinline__ void wave_upper_tn(const float* X, const float* Y, bo
 }
 
 // D[row][col] of a 16x16x4 result sits in lane col + 16 * (row / 4), register row % 4.
-template <int NP>
+// SYM: the blocks below the diagonal too, as the transposes (a symmetric product).
+template <int NP, bool SYM = false>
 __device__ __forceinline__ void wave_store_upper(float* W, int lane,
                                                  const f32x4v (&acc)[SmallLayout<NP>::G][(NP / 16) * (NP / 16 + 1) / 2]) {
   using Lay = SmallLayout<NP>;
@@ -189,8 +211,10 @@ __device__ __forceinline__ void wave_store_upper(float* W, int lane,
 #pragma unroll
       for (int bj = bi; bj < NB; ++bj) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
+        for (int e = 0; e < 4; ++e) {
           W[g * Lay::MAT + (16 * bi + 4 * q4 + e) * Lay::LD + 16 * bj + l16] = acc[g][u][e];
+          if (SYM && bj > bi) W[g * Lay::MAT + (16 * bj + l16) * Lay::LD + 16 * bi + 4 * q4 + e] = acc[g][u][e];
+        }
         ++u;
       }
   }
@@ -208,6 +232,11 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_small(SmallArgs a) {
   if (mat0 >= a.batch) return;  // the whole wave is idle; the kernel has no workgroup barrier
   const int n = a.n, mat = mat0 + g;
   const bool live = r < n;
+  // one matrix per wave: row broadcasts by readlane (RL); two or four: through LDS slots (with
+  // two groups the readlanes and selects cost more than the LDS round trips they replace:
+  // 4096 x 32, 85 -> 102 us)
+  constexpr bool RL = G == 1;
+  const bool gup = g == 1;  // RL with two groups: this lane's group is the upper one
   float* As = smem + wid * Lay::PER_WAVE;
   float* Ws = As + G * MAT;
   float* Sl = Ws + G * MAT;
@@ -259,8 +288,15 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_small(SmallArgs a) {
       int bi = cand ? pos : INT_MAX;
       group_argmax<NP>(babs, bv, bi);
       const bool win = cand && pos == bi;
-      if (win) lds_store_row<NP, (j + 1) / 4>(myS, x);
-      wave_lds_order();
+      int pw[RL ? G : 1];  // RL: the winning lane of each group (one per group), uniform
+      if constexpr (RL) {
+        const uint64_t wm = __ballot(win);
+        pw[0] = __builtin_amdgcn_readfirstlane(__ffsll((long long)(G == 1 ? wm : (wm & 0xffffffffull))) - 1);
+        if constexpr (G == 2) pw[G - 1] = __builtin_amdgcn_readfirstlane(__ffsll((long long)(wm >> 32)) + 31);
+      } else {
+        if (win) lds_store_row<NP, (j + 1) / 4>(myS, x);
+        wave_lds_order();
+      }
       // LAPACK xGETRF2: scale by the reciprocal unless the pivot is subnormal; a zero pivot
       // (all-zero column) leaves the column as it is
       const float pv = bv;
@@ -275,8 +311,12 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_small(SmallArgs a) {
         }
       }
       pos = win ? j : (pos == j ? bi : pos);
-      rank1_from_slot<NP, j>(x, l, myS);
-      wave_lds_order();  // the next column's slot store stays behind these reads
+      if constexpr (RL) {
+        rank1_from_lanes<NP, G, j>(x, l, pw, gup);  // the winner's own l is 0
+      } else {
+        rank1_from_slot<NP, j>(x, l, myS);
+        wave_lds_order();  // the next column's slot store stays behind these reads
+      }
     }
   });
   // unit-lower L in A's row order: row r of the factor sits at logical position pos
@@ -295,7 +335,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_small(SmallArgs a) {
       f32x4v acc[G][NBU];
       wave_upper_tn<NP>(Ws, Ws, true, lane, acc);
       wave_lds_order();
-      wave_store_upper<NP>(Ws, lane, acc);
+      wave_store_upper<NP, RL>(Ws, lane, acc);  // RL: whole (symmetric), the Cholesky reads both halves
     }
     wave_lds_order();
     // jitter: mu = 1e-7 * mean(diag G), added to the diagonal (reflection_no_reflectors.py:74-75)
@@ -313,22 +353,41 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_small(SmallArgs a) {
       if (j < n) {
         int rr = r;
         asm volatile("" : "+v"(rr));
-        if (rr == j) {
-          const float d = gr[j];
-          if (!(d > 0.f)) f = j;
+        if constexpr (RL) {
+          // G' is held whole (symmetric): lane r's G'[r][j] is G'[j][r], so R[j][r] / R[j][j] =
+          // G'[r][j] / G'[j][j] is lane-local and only row j's raw values are broadcast (read
+          // before lane j scales its row)
+          int pj[G];
+          pj[0] = j;
+          if constexpr (G == 2) pj[G - 1] = NP + j;
+          const float d = group_bcast<G>(gr[j], pj, gup);
           const float rjj = sqrtf(d), rinv = 1.f / rjj;
-          gr[j] = rjj;
+          if (rr > j && rr < n) rank1_from_lanes<NP, G, j>(gr, (gr[j] * rinv) * rinv, pj, gup);
+          if (rr == j) {
+            if (!(d > 0.f)) f = j;
+            gr[j] = rjj;
 #pragma unroll
-          for (int c = j + 1; c < NP; ++c) gr[c] *= rinv;
-          lds_store_row<NP, j / 4>(myS, gr);
-          myD[j] = rinv;
+            for (int c = j + 1; c < NP; ++c) gr[c] *= rinv;
+            myD[j] = rinv;
+          }
+        } else {
+          if (rr == j) {
+            const float d = gr[j];
+            if (!(d > 0.f)) f = j;
+            const float rjj = sqrtf(d), rinv = 1.f / rjj;
+            gr[j] = rjj;
+#pragma unroll
+            for (int c = j + 1; c < NP; ++c) gr[c] *= rinv;
+            lds_store_row<NP, j / 4>(myS, gr);
+            myD[j] = rinv;
+          }
+          wave_lds_order();
+          if (rr > j && rr < n) {
+            const float rj = myS[rr];  // R[j][r]
+            rank1_from_slot<NP, j>(gr, rj, myS);
+          }
+          wave_lds_order();
         }
-        wave_lds_order();
-        if (rr > j && rr < n) {
-          const float rj = myS[rr];  // R[j][r]
-          rank1_from_slot<NP, j>(gr, rj, myS);
-        }
-        wave_lds_order();
       }
     });
     f = group_min<NP>(f);
@@ -374,9 +433,17 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_small(SmallArgs a) {
     if (k < n) {
       int rr = r;
       asm volatile("" : "+v"(rr));
-      if (rr == k) lds_store_row<NP, k / 4>(myS, x);
-      wave_lds_order();
-      const float d = myS[k];
+      int pk[G];
+      pk[0] = k;
+      if constexpr (G > 1) pk[1] = NP + k;
+      float d;
+      if constexpr (RL) {
+        d = group_bcast<G>(x[k], pk, gup);
+      } else {
+        if (rr == k) lds_store_row<NP, k / 4>(myS, x);
+        wave_lds_order();
+        d = myS[k];
+      }
       const float pp = 1.f - d, pm = 1.f + d;
       const bool plus = fabsf(pp) >= fabsf(pm);  // |1-d| >= |1+d|, the tie d = 0 takes +1
       const float sk = plus ? 1.f : -1.f;
@@ -385,9 +452,10 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_small(SmallArgs a) {
       if (rr > k && rr < n) {
         const float mult = (-sk * x[k]) / piv;
         x[k] = mult;
-        rank1_from_slot<NP, k>(x, mult, myS);
+        if constexpr (RL) rank1_from_lanes<NP, G, k>(x, mult, pk, gup);
+        else rank1_from_slot<NP, k>(x, mult, myS);
       }
-      wave_lds_order();
+      if constexpr (!RL) wave_lds_order();
     }
   });
 
