@@ -266,8 +266,6 @@ int launch_chol(float* G, int64_t sg, float* Dinv, int* info, int64_t batch, int
   a.keep_info = keep_info ? 1 : 0;
   a.Wm = Wm; a.sw = (int64_t)n * n;
   if (lu_split(batch, n)) {
-    // small batch: per 64-column block a diagonal launch (one wave per matrix), then the
-    // block row and the trailing tiles spread over one wave per 32 columns / per tile
     // small batch: the first diagonal block, then per 64-column block the block row (one wave
     // per 32 columns) and one launch that runs the trailing tiles (one wave per tile) beside the
     // next diagonal block's update and factor (one workgroup per matrix)
