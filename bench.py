@@ -55,9 +55,9 @@ def stage_symbols(batch: int, n: int) -> dict:
     vec4 = n % 4 == 0
     tf = lambda b: "true" if b else "false"  # noqa: E731
     if split:
-        rpt = 2 if n <= 1024 else 4
-        lu = f"rnr::k_lu<true, 32, {rpt}, true, 512> + rnr::k_lu_trail_g<true, 1..4>"
-        chart = f"rnr::k_lu<false, 32, {rpt}, true, 512> + rnr::k_lu_trail_g<false, 1..4> + rnr::k_chart_tau"
+        rpt = 1 if n <= 1024 else 2
+        lu = f"rnr::k_lu<true, 32, {rpt}, true, 1024> + rnr::k_lu_trail_g<true, 1..4>"
+        chart = f"rnr::k_lu<false, 32, {rpt}, true, 1024> + rnr::k_lu_trail_g<false, 1..4> + rnr::k_chart_tau"
         chol = "rnr::k_chol_jitter + rnr::k_chol_diag + rnr::k_chol_row + rnr::k_chol_step"
     else:
         nb, rpt = (64, 1) if n <= 512 else ((32, 2) if n <= 1024 else (16, 4))

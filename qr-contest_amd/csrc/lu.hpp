@@ -119,7 +119,7 @@ __device__ __forceinline__ void lu_inverse_wave(float* P, const float* LT, int l
 // T: threads per workgroup (512; 128 or 256 for n <= 128 / 256 with 64-wide panels, so that
 // small matrices do not hold idle waves and several workgroups share a CU).
 template <bool PIVOT, int NB, int RPT, bool SPLIT = false, int T = kLuThreads>
-__global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_lu(LuArgs a) {
+__global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(T > 512 ? 4 : 2))) void k_lu(LuArgs a) {
   constexpr int NW = T / 64;
   constexpr int NB4 = NB / 4;
   constexpr int LDP = NB + 1;

@@ -142,13 +142,15 @@ void launch_lu_trail_g(const LuArgs& a, int S, int kg, int cb, int ce, int64_t b
 
 // 32-wide panels in groups of four: panel s of a group is first brought up to date with the
 // group's earlier panels (its 32 columns only), then factored (L11^-1 to slot s of the xbuf);
-// after the group one rank-128 pass updates everything right of it.
+// after the group one rank-128 pass updates everything right of it.  The panel launches run
+// 1024 threads (16 waves, RPT rows each): one workgroup per matrix leaves most CUs idle here,
+// so each column step's per-thread work is what sets the time.
 template <bool PIVOT, int RPT>
 int launch_lu_split(LuArgs a, int64_t batch, hipStream_t st) {
-  constexpr int NB = 32, G = 4;
+  constexpr int NB = 32, G = 4, T = 1024;
   const size_t lds = lu_lds_bytes(a.n, NB, true);  // the panel's rows stay out of LDS (L11 only)
   if (lds > kLdsMax) return RNR_ERR_UNSUPPORTED_N;
-  if (int e = set_lds(k_lu<PIVOT, NB, RPT, true>, lds)) return e;
+  if (int e = set_lds(k_lu<PIVOT, NB, RPT, true, T>, lds)) return e;
   const int n = a.n;
   float* const xbase = a.X;
   for (int kg = 0; kg < n; kg += G * NB) {
@@ -159,7 +161,7 @@ int launch_lu_split(LuArgs a, int64_t batch, hipStream_t st) {
       if (sp > 0) launch_lu_trail_g<PIVOT>(a, sp, kg, kp, min(kp + NB, n), batch, st);
       a.k0 = kp;
       a.X = xbase + (int64_t)sp * batch * NB * NB;
-      k_lu<PIVOT, NB, RPT, true><<<dim3((unsigned)batch), dim3(kLuThreads), lds, st>>>(a);
+      k_lu<PIVOT, NB, RPT, true, T><<<dim3((unsigned)batch), dim3(T), lds, st>>>(a);
     }
     a.X = xbase;
     if (kg + G * NB < n) launch_lu_trail_g<PIVOT>(a, G, kg, kg + G * NB, n, batch, st);
@@ -184,8 +186,8 @@ int launch_lu(bool pivot, const float* src, int64_t ss, float* dst, int64_t sd, 
   if (lu_split(batch, n) && xbuf) {
     // 32-wide panels at every split size: the panel's rows go straight between HBM and registers,
     // so its width is not bound by an n-row LDS copy (rank-32 trailing updates, half the passes)
-    if (pivot) return n <= 1024 ? launch_lu_split<true, 2>(a, batch, st) : launch_lu_split<true, 4>(a, batch, st);
-    return n <= 1024 ? launch_lu_split<false, 2>(a, batch, st) : launch_lu_split<false, 4>(a, batch, st);
+    if (pivot) return n <= 1024 ? launch_lu_split<true, 1>(a, batch, st) : launch_lu_split<true, 2>(a, batch, st);
+    return n <= 1024 ? launch_lu_split<false, 1>(a, batch, st) : launch_lu_split<false, 2>(a, batch, st);
   }
   // rows per thread: n <= T * RPT; one row per thread with 128 or 256 threads at n <= 128 / 256
   if (pivot) {
