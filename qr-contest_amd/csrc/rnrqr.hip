@@ -126,9 +126,10 @@ void launch_lu_trail_g(const LuArgs& a, int S, int kg, int cb, int ce, int64_t b
   const int rb = kg + 32 * S, rows = a.n - rb;
   const int nchunk = (ce - cb + 63) / 64;
   // rows per workgroup: each workgroup forms its chunk's U itself, so it takes as many rows as
-  // still leaves about 2 workgroups per CU (at least 256)
+  // still leaves about one workgroup per two CUs (at least 256; measured at 16 x 2048 against
+  // thresholds of 2 to 8 workgroups per CU, which redo the U more often: 20.0 -> 19.5 ms)
   int rpw = kLuTrailRows;
-  while (rpw < rows && batch * nchunk * ((rows + 2 * rpw - 1) / (2 * rpw)) >= 512) rpw *= 2;
+  while (rpw < rows && batch * nchunk * ((rows + 2 * rpw - 1) / (2 * rpw)) >= 128) rpw *= 2;
   const int nrg = (rows + rpw - 1) / rpw;
   const dim3 grid((unsigned)(batch * nchunk * nrg)), block(kLuTrailThreads);
   const int64_t xslot = batch * 1024;
