@@ -46,96 +46,66 @@ inline size_t chol_lds_bytes(int n, bool strip) {
 // Wave 0: factor the 64x64 diagonal block held in D (symmetric; the upper part is read) in
 // place into R (upper, zeros below), with R also written column-major into RT (RT[c][k] =
 // R[k][c], row stride 68) and 1 / R[j][j] into RI; returns the first non-positive pivot
-// (column index, or INT_MAX).  Lane i holds symmetric row i of the block in four named
-// 16-wide vectors (compile-time element access keeps them in VGPRs).  Step j: lane c holds
-// G'[j][c] = G'[c][j], so the scaled pivot row R[j][c] = G'[j][c] / r sits in lane c; it is
-// broadcast through an LDS row SB[j % 2] (two rows: SB holds 2 x 64 floats), all of whose
-// reads issue together.  The steps are software-pipelined: step j first updates column j + 1
-// only, which is all step j + 1's pivot needs, then forms step j + 1's pivot and issues its
-// broadcast, and only then updates its remaining columns -- so step j + 1's LDS round trip
-// runs under step j's FMAs instead of after them.  A wave issues its LDS operations in order;
-// wave_lds_order keeps the compiler from moving them, so no barrier sits on the chain.  The
-// pivot's square root and reciprocal are the hardware's (1 ulp).
+// (column index, or INT_MAX).  The block lives in MFMA accumulators -- the diagonal 32x32
+// blocks (0,0) and (1,1) as the two blocks of one v_mfma_f32_32x32x1_2b_f32 result, the
+// upper off-diagonal block (0,1) as one 32x32x2 result (the lower one is never read) -- and
+// each step's rank-1 update G -= u u^T is two MFMAs:
+//   * the pivot G[j][j] is read from its accumulator lane (readlane), r = sqrt, 1 / r;
+//   * row j of G sits in one accumulator register per block, in the lanes of one half-wave:
+//     v_permlane32_swap gathers it as lane c -> G[j][c] (c = 0..63) and it is scaled to the row
+//     of R (r at c = j, zero below);
+//   * u (the row past j) is the A and B operand of the 2-block product for (0,0) and (1,1), and
+//     with its halves swapped the B operand of the 32x32x2 product for (0,1).
+// So a step is a chain of MFMA -> readlane -> sqrt / rcp -> swap -> MFMA with no LDS round trip
+// and no per-lane loop over the row; rows of R go to LDS as they finish.  SB is unused here.
+// The pivot's square root and reciprocal are the hardware's (1 ulp).
 __device__ __forceinline__ int chol_diag_wave(float* D, float* RT, float* RI, float* SB, int lane) {
+  (void)SB;
   asm volatile("" : "+v"(lane));  // lane-derived values stay here, not hoisted out of the caller's loop
-  f32x16 v0, v1, v2, v3;
-  auto V = [&](auto qc) -> f32x16& {
-    constexpr int q = decltype(qc)::value;
-    if constexpr (q == 0) return v0;
-    else if constexpr (q == 1) return v1;
-    else if constexpr (q == 2) return v2;
-    else return v3;
-  };
-  static_for<0, 4>([&](auto qc) {
-    constexpr int q = decltype(qc)::value;
-    f32x16& v = V(qc);
+  f32x32 dg;  // (0,0) in registers 0..15, (1,1) in 16..31
+  f32x16 od;  // (0,1)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int c = 16 * q + e;
-      v[e] = D[(c >= lane) ? lane * 65 + c : c * 65 + lane];
-    }
-  });
-  // v[c] -= sm * pv for one compile-time column c
-  auto upd = [&](auto cc, float sm, float pv) {
-    constexpr int c = decltype(cc)::value;
-    V(std::integral_constant<int, c / 16>{})[c % 16] -= sm * pv;
-  };
+  for (int r = 0; r < 32; ++r) {
+    const int bb = r >> 4, i = 32 * bb + acc_row(r & 15, lane), c = 32 * bb + (lane & 31);
+    dg[r] = D[(i <= c) ? i * 65 + c : c * 65 + i];
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) od[r] = D[acc_row(r, lane) * 65 + 32 + (lane & 31)];
   int fail = INT_MAX;
-  // head of step j: the pivot (column j, already final), this lane's scaled row value si and
-  // update multiplier sm, the broadcast into SB[j % 2]
-  float si = 0.f, sm = 0.f, rinv = 0.f;
-  auto head = [&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
-    const float rjj = V(std::integral_constant<int, j / 16>{})[j % 16];
-    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rjj), j));
-    if (!(d > 0.f) && fail == INT_MAX) fail = j;
-    const float r = __builtin_amdgcn_sqrtf(d);
-    rinv = __builtin_amdgcn_rcpf(r);
-    si = (ln == j) ? r : rjj * rinv;  // lane c > j: R[j][c]
-    sm = (ln > j) ? si : 0.f;         // rows below j take the update
-    SB[(j & 1) * 64 + ln] = si;
-    wave_lds_order();
-  };
-  // the broadcast row of the current step (float4 units from column 4 * ((j + 1) / 4) on)
-  float4 pc[16];
-  auto read_row = [&](auto jc, float4 (&dst)[16]) {
-    constexpr int j = decltype(jc)::value;
-    constexpr int C0 = (j + 1) / 4;
-    const lds_f4* sbp = lds_base(SB + (j & 1) * 64);
-#pragma unroll
-    for (int c4 = C0; c4 < 16; ++c4) dst[c4] = lds_get(sbp, c4);
-  };
-  auto pget = [&](const float4 (&row)[16], auto cc) -> float {
-    constexpr int c = decltype(cc)::value;
-    return f4get<c % 4>(row[c / 4]);
-  };
-  head(std::integral_constant<int, 0>{});
-  read_row(std::integral_constant<int, 0>{}, pc);
   static_for<0, 64>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
+    constexpr int B = j / 32, I = j % 32, HJ = (I / 4) % 2, RR = 4 * (I / 8) + I % 4;
     int ln = lane;
-    asm volatile("" : "+v"(ln));
-    // row j of R from this step's values (lane ln: R[j][ln])
-    const float rj = (ln >= j) ? si : 0.f;
-    const float smj = sm, rinvj = rinv;
-    if constexpr (j + 1 < 64) {
-      // column j + 1 first: step j + 1's pivot and broadcast depend on it alone
-      upd(std::integral_constant<int, j + 1>{}, smj, pget(pc, std::integral_constant<int, j + 1>{}));
-      head(std::integral_constant<int, j + 1>{});
-      float4 pn[16];
-      read_row(std::integral_constant<int, j + 1>{}, pn);  // in flight during the rest of step j
-      // the rest of step j's update
-      static_for<j + 2, 64>([&](auto cc) { upd(cc, smj, pget(pc, cc)); });
-#pragma unroll
-      for (int c4 = (j + 2) / 4; c4 < 16; ++c4) pc[c4] = pn[c4];
+    asm volatile("" : "+v"(ln));  // the step's lane masks are formed here, not hoisted
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dg[16 * B + RR]), I + 32 * HJ));
+    if (!(d > 0.f) && fail == INT_MAX) fail = j;
+    const float r = __builtin_amdgcn_sqrtf(d);
+    const float rinv = __builtin_amdgcn_rcpf(r);
+    // lane c: G[j][c] (columns below j are masked out below)
+    float v;
+    if constexpr (B == 0) {
+      const float2 p = lane_halves(dg[RR], od[RR]);
+      v = HJ == 0 ? p.x : p.y;
+    } else if constexpr (HJ == 1) {
+      v = dg[16 + RR];
+    } else {
+      v = lane_halves(0.f, dg[16 + RR]).x;
+    }
+    const float rv = (ln == j) ? r : v * rinv;
+    const float rj = (ln >= j) ? rv : 0.f;  // row j of R
+    if constexpr (j < 63) {
+      const float u = (ln > j) ? rv : 0.f;
+      dg = mfma_2b(-u, u, dg);
+      if constexpr (j < 31) {  // rows of block row 0 below j remain
+        const float2 q = lane_halves(u, u);  // .y: u[32 + (l % 32)]
+        od = mfma((ln < 32) ? -u : 0.f, q.y, od);
+      }
     }
     D[j * 65 + ln] = rj;   // row j of R
     RT[ln * 68 + j] = rj;  // column ln of R
-    RI[j] = rinvj;         // same value from every lane
-    wave_lds_order();      // a later step's SB store stays behind this step's reads
+    RI[j] = rinv;          // same value from every lane
   });
+  wave_lds_order();
   return fail;
 }
 

@@ -17,6 +17,23 @@ __device__ __forceinline__ f32x16 mfma(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+
+// v_mfma_f32_32x32x1_2b_f32: two independent 32x32 outer products, D_b = A_b B_b + C_b.
+// Block b takes A_b[i] from lane 32 b + i and B_b[j] from lane 32 b + j; its result sits in
+// registers 16 b .. 16 b + 15 with the layout of mfma above (D_b[row][col] in lane
+// col + 32 * ((row / 4) % 2), register 16 b + 4 * (row / 8) + row % 4).
+__device__ __forceinline__ f32x32 mfma_2b(float a, float b, f32x32 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0);
+}
+
+// v_permlane32_swap of (x, y): returns [x lanes 0-31, y lanes 0-31] in .x and
+// [x lanes 32-63, y lanes 32-63] in .y (lane l < 32 of the result's upper half reading l + 32).
+__device__ __forceinline__ float2 lane_halves(float x, float y) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  return make_float2(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
 __device__ __forceinline__ int acc_row(int r, int lane) {
   return ((r >> 2) << 3) + ((lane >> 5) << 2) + (r & 3);
 }
