@@ -77,8 +77,8 @@ def stage_symbols(batch: int, n: int) -> dict:
             bk, lv = 32, True
         return f"rnr::k_tn_upper<{bm}, {tf(closure)}, {tf(closure)}, {tf(vec4)}, {bk}, {tf(lv)}>"
 
-    rb = 64 if batch * ((n + 127) // 128) < 512 else 128
-    trsm = f"rnr::k_trsm<{tf(vec4)}, {rb}>"
+    half = batch * ((n + 127) // 128) < 512  # 64-row blocks, K split over two wave groups
+    trsm = f"rnr::k_trsm<{tf(vec4)}, 64, 2>" if half else f"rnr::k_trsm<{tf(vec4)}, 128, 1>"
     wblk = "rnr::k_wblocks" if split else chol  # the fused Cholesky forms the W blocks itself
     return {"lu": lu, "gram_L": tn(False, True), "chol_1": chol, "wblk_1": wblk, "trsm_1": trsm,
             "gram_Q1": tn(False, False), "chol_2": chol, "wblk_2": wblk, "trsm_2": trsm,

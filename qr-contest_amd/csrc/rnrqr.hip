@@ -315,9 +315,9 @@ int launch_trsm(const float* M, int64_t sm, const int* mperm, const float* Wm, i
   const bool vec4 = (n % 4 == 0) && (sq % 4 == 0) && (sm % 4 == 0) && aligned(Q, 16) && aligned(M, 16) &&
                     aligned(Wm, 16);
   const dim3 grid((unsigned)total), block(256);
-  if (half) {
-    if (vec4) k_trsm<true, 64><<<grid, block, 0, st>>>(a);
-    else k_trsm<false, 64><<<grid, block, 0, st>>>(a);
+  if (half) {  // and each block column's K split over two groups of waves
+    if (vec4) k_trsm<true, 64, 2><<<grid, dim3(512), 0, st>>>(a);
+    else k_trsm<false, 64, 2><<<grid, dim3(512), 0, st>>>(a);
   } else {
     if (vec4) k_trsm<true, kTrsmRows><<<grid, block, 0, st>>>(a);
     else k_trsm<false, kTrsmRows><<<grid, block, 0, st>>>(a);

@@ -134,18 +134,24 @@ __global__ __launch_bounds__(256) void k_wblocks(WblkArgs a) {
 
 // RB = 128: each wave owns 32 rows x 64 columns (two 32x32 accumulators); RB = 64 (small
 // batches at large n, twice the workgroups): 2 x 2 waves of 32 x 32.
-template <bool VEC4, int RB = kTrsmRows>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_trsm(TrsmArgs a) {
+// SK = 2 (small batches at large n, where one 256-thread workgroup per row block leaves two
+// waves per SIMD): 512 threads, two groups of four waves splitting each block column's K
+// chunks between them (group g takes chunks g, g + 2, ...), group 1's sums added into group
+// 0's through LDS before group 0 stores -- twice the waves for the same row blocks.
+template <bool VEC4, int RB = kTrsmRows, int SK = 1>
+__global__ __launch_bounds__(256 * SK) __attribute__((amdgpu_waves_per_eu(4))) void k_trsm(TrsmArgs a) {
   constexpr int BK = 16, LDA = BK + 1;
   constexpr int NP = RB / 64;    // A-chunk float4 slots per thread
   constexpr int WN = 128 / RB;   // waves side by side across the 64 columns
   constexpr int NACC = 2 / WN;   // 32x32 accumulators per wave
-  __shared__ __attribute__((aligned(16))) float smA[2 * RB * LDA];  // A chunk: RB rows x BK
-  __shared__ __attribute__((aligned(16))) float smB[2 * BK * 64];   // B chunk: BK x 64
+  __shared__ __attribute__((aligned(16))) float smA[2 * SK * RB * LDA];  // A chunks: RB rows x BK
+  __shared__ __attribute__((aligned(16))) float smB[2 * SK * BK * 64];   // B chunks: BK x 64
   __shared__ __attribute__((aligned(16))) int prow[RB];
   __shared__ int mrow[RB];
+  __shared__ float red[SK == 2 ? 4 * NACC * 16 * 64 : 1];  // group 1's accumulators (SK = 2)
 
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int ttid = threadIdx.x, grp = SK == 2 ? ttid >> 8 : 0;
+  const int tid = ttid & 255, lane = tid & 63, wid = tid >> 6;  // within the group
   const int l32 = lane & 31, h = lane >> 5, wr = (wid / WN) * 32, wc = (wid % WN) * 32 * NACC;
   const int pid = xcd_remap(blockIdx.x, a.total);
   const int b = pid / a.nrb, r0 = (pid - b * a.nrb) * RB, n = a.n;
@@ -155,7 +161,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   float* Q = a.Q + b * a.sq;
   float* Q2 = a.Q2 ? a.Q2 + b * a.sq2 : nullptr;
 
-  if (tid < RB) {
+  if (ttid < RB) {
     const int row = r0 + tid;
     prow[tid] = (row < n) ? (a.perm ? a.perm[(int64_t)b * n + row] : row) : 0;
     mrow[tid] = (row < n) ? (a.mperm ? a.mperm[(int64_t)b * n + row] : row) : 0;
@@ -221,8 +227,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     }
   };
   auto lstore = [&](int buf, int kc, int c0) {
-    float* As = smA + buf * RB * LDA;
-    float* Bs = smB + buf * BK * 64;
+    float* As = smA + (buf * SK + grp) * RB * LDA;
+    float* Bs = smB + (buf * SK + grp) * BK * 64;
     if (kc >= c0) {  // uniform: the diagonal chunk
       if (a.mperm) {  // L[row][k]: stored below the diagonal, 1 on it, 0 above
 #pragma unroll
@@ -249,24 +255,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 #pragma unroll
     for (int j = 0; j < NACC; ++j) acc[j] = zero16();
     int buf = 0;
-    gload(0, c0);
-    lstore(0, 0, c0);
+    // this group's chunks: K = kc0, kc0 + SK BK, ... (uniform per group)
+    const int kc0 = grp * BK;
+    if (kc0 < kend) {
+      gload(kc0, c0);
+      lstore(0, kc0, c0);
+    }
     __syncthreads();
-    for (int kc = 0; kc < kend; kc += BK) {
-      const bool more = kc + BK < kend;
-      if (more) gload(kc + BK, c0);
-      const float* As = smA + buf * RB * LDA;
-      const float* Bs = smB + buf * BK * 64;
+    for (int kb = 0; kb < kend; kb += SK * BK) {
+      const int kc = kb + kc0;
+      const bool more = kc + SK * BK < kend;
+      if (more) gload(kc + SK * BK, c0);
+      if (kc < kend) {
+        const float* As = smA + (buf * SK + grp) * RB * LDA;
+        const float* Bs = smB + (buf * SK + grp) * BK * 64;
 #pragma unroll
-      for (int kk = 0; kk < BK; kk += 2) {
-        const int k = kk + h;
-        const float av = As[(wr + l32) * LDA + k];
+        for (int kk = 0; kk < BK; kk += 2) {
+          const int k = kk + h;
+          const float av = As[(wr + l32) * LDA + k];
 #pragma unroll
-        for (int j = 0; j < NACC; ++j) acc[j] = mfma(av, Bs[k * 64 + wc + 32 * j + l32], acc[j]);
+          for (int j = 0; j < NACC; ++j) acc[j] = mfma(av, Bs[k * 64 + wc + 32 * j + l32], acc[j]);
+        }
       }
-      if (more) lstore(buf ^ 1, kc + BK, c0);
+      if (more) lstore(buf ^ 1, kc + SK * BK, c0);
       __syncthreads();
       buf ^= 1;
+    }
+    if constexpr (SK == 2) {
+      if (grp == 1) {
+#pragma unroll
+        for (int j = 0; j < NACC; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) red[((wid * NACC + j) * 16 + r) * 64 + lane] = acc[j][r];
+      }
+      __syncthreads();
+      if (grp == 0) {
+#pragma unroll
+        for (int j = 0; j < NACC; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[j][r] += red[((wid * NACC + j) * 16 + r) * 64 + lane];
+      }
     }
     // accumulator registers 4g .. 4g + 3 hold the consecutive rows wr + 8g + 4h + (0..3):
     // their targets come from one 16-byte LDS read; full tiles store without masks
@@ -287,12 +315,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
           }
       }
     };
-    if (r0 + RB <= n && c0 + 64 <= n) {  // uniform
-      store_tile(Q, std::false_type{});
-      if (Q2) store_tile(Q2, std::false_type{});
-    } else {
-      store_tile(Q, std::true_type{});
-      if (Q2) store_tile(Q2, std::true_type{});
+    if (grp == 0) {
+      if (r0 + RB <= n && c0 + 64 <= n) {  // uniform
+        store_tile(Q, std::false_type{});
+        if (Q2) store_tile(Q2, std::false_type{});
+      } else {
+        store_tile(Q, std::true_type{});
+        if (Q2) store_tile(Q2, std::true_type{});
+      }
     }
     // the next block column reads these outputs back (other threads of this workgroup)
     __syncthreads();
