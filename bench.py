@@ -52,6 +52,7 @@ def stage_symbols(batch: int, n: int) -> dict:
         np_ = 16 if n <= 16 else (32 if n <= 32 else 64)
         return {"path": f"rnr::k_small<{np_}>"}
     split = n > 512 and batch < 128
+    csplit = split or n <= 128  # the Cholesky's per-block form
     vec4 = n % 4 == 0
     tf = lambda b: "true" if b else "false"  # noqa: E731
     if split:
@@ -60,11 +61,13 @@ def stage_symbols(batch: int, n: int) -> dict:
         chart = f"rnr::k_lu<false, 32, {rpt}, true, 1024> + rnr::k_lu_trail_g<false, 1..4> + rnr::k_chart_tau"
         chol = "rnr::k_chol_jitter + rnr::k_chol_diag + rnr::k_chol_row + rnr::k_chol_step"
     else:
-        nb, rpt = (64, 1) if n <= 512 else ((32, 2) if n <= 1024 else (16, 4))
+        nb, rpt = (32, 1) if n <= 128 else ((64, 1) if n <= 512 else ((32, 2) if n <= 1024 else (16, 4)))
         t = 128 if n <= 128 else (256 if n <= 256 else 512)  # workgroup size (launch_lu)
         lu = f"rnr::k_lu<true, {nb}, {rpt}, false, {t}>"
         chart = f"rnr::k_lu<false, {nb}, {rpt}, false, {t}>"
         chol = f"rnr::k_chol<{256 if n <= 256 else 512}>"
+    if csplit:
+        chol = "rnr::k_chol_jitter + rnr::k_chol_diag + rnr::k_chol_row + rnr::k_chol_step"
     big = n > 256
     bm = 128 if big else 64
 
@@ -79,7 +82,7 @@ def stage_symbols(batch: int, n: int) -> dict:
 
     half = batch * ((n + 127) // 128) < 512  # 64-row blocks, K split over two wave groups
     trsm = f"rnr::k_trsm<{tf(vec4)}, 64, 2>" if half else f"rnr::k_trsm<{tf(vec4)}, 128, 1>"
-    wblk = "rnr::k_wblocks" if split else chol  # the fused Cholesky forms the W blocks itself
+    wblk = "rnr::k_wblocks" if csplit else chol  # the fused Cholesky forms the W blocks itself
     return {"lu": lu, "gram_L": tn(False, True), "chol_1": chol, "wblk_1": wblk, "trsm_1": trsm,
             "gram_Q1": tn(False, False), "chol_2": chol, "wblk_2": wblk, "trsm_2": trsm,
             "chart": chart, "closure": tn(True, False)}
