@@ -342,12 +342,49 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_small(SmallArgs a) {
     const float dg = live ? myW[r * LD + r] : 0.f;
     const float mu = 1e-7f * (group_sum<NP>(dg) / (float)n);
     if (live) myW[r * LD + r] = dg + mu;
+    int f = INT_MAX;
+    if constexpr (G == 2) {
+      // two matrices per wave: their G' are the two blocks of one v_mfma_f32_32x32x1_2b_f32
+      // accumulator (block g from lanes 32 g ..), and each step's rank-1 update G' -= u u^T of
+      // both is one MFMA: the pivots are read from their accumulator lanes, row j of each
+      // block (one register, one half-wave) is gathered into lane order with a permlane32
+      // swap and scaled into row j of R, which goes straight to R^T in Ws
+      wave_lds_order();  // the jitter's diagonal stores before these reads of other lanes' rows
+      f32x32 acc;
+#pragma unroll
+      for (int q = 0; q < 32; ++q) {
+        const int i = acc_row(q & 15, lane), c = lane & 31;
+        acc[q] = Ws[(q >> 4) * MAT + ((i <= c) ? i * LD + c : c * LD + i)];  // upper part of G'
+      }
+      wave_lds_order();  // the R^T stores below stay behind these reads
+      static_for<0, NP>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        constexpr int HJ = (j / 4) % 2, RR = 4 * (j / 8) + j % 4;
+        if (j < n) {
+          int rr = r;
+          asm volatile("" : "+v"(rr));  // the step's lane masks are formed here, not hoisted
+          const float d0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc[RR]), j + 32 * HJ));
+          const float d1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc[16 + RR]), j + 32 * HJ));
+          const float d = gup ? d1 : d0;
+          if (!(d > 0.f) && f == INT_MAX) f = j;
+          const float rjj = sqrtf(d), rinv = 1.f / rjj;
+          const float2 p = lane_halves(acc[RR], acc[16 + RR]);
+          const float v = HJ == 0 ? p.x : p.y;  // lane c of group g: G'_g[j][c]
+          const float rv = (rr == j) ? rjj : v * rinv;
+          if (j + 1 < n) {
+            const float u = (rr > j) ? rv : 0.f;
+            acc = mfma_2b(-u, u, acc);
+          }
+          myW[rr * LD + j] = (rr >= j) ? rv : 0.f;  // R^T[c][j] = R[j][c]
+          if (rr == j) myD[j] = rinv;
+        }
+      });
+    } else {
     float gr[NP];
     lds_load_row<NP>(gr, myW + r * LD);  // upper part of row r of G (+ mu I)
     wave_lds_order();
 
     // upper Cholesky on the rows: step j broadcasts row j of R = G'[j][j:] / sqrt(G'[j][j])
-    int f = INT_MAX;
     static_for<0, NP>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
       if (j < n) {
@@ -390,14 +427,14 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_small(SmallArgs a) {
         }
       }
     });
-    f = group_min<NP>(f);
-    if (pass == 0) fail0 = f; else fail1 = f;
-
     // R^T -> Ws (column c of R contiguous), then x <- x R^-1 by forward substitution.  Rows
     // of G past n are zero, so R^T is zero there; 1 / R[c][c] is 1 past n: the padded
     // columns of x stay zero and need no test.
 #pragma unroll
     for (int c = 0; c < NP; ++c) myW[c * LD + r] = gr[c];
+    }
+    f = group_min<NP>(f);
+    if (pass == 0) fail0 = f; else fail1 = f;
     wave_lds_order();
     static_for<0, NP>([&](auto cc) {
       constexpr int c = decltype(cc)::value;
