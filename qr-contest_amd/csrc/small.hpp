@@ -64,9 +64,25 @@ __device__ __forceinline__ f32x4v mfma16x4(float a, float b, f32x4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// The value of lane l ^ 16 (v_permlane16_swap of v with itself: .x holds rows 0, 0, 2, 2 of
+// 16 lanes, .y rows 1, 1, 3, 3) and of lane l ^ 32 (v_permlane32_swap: .x the low half twice,
+// .y the high half twice) -- VALU lane exchanges, no LDS round trip.
+__device__ __forceinline__ uint32_t lane_xor16(uint32_t v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (__lane_id() & 16) ? p[0] : p[1];
+}
+__device__ __forceinline__ uint32_t lane_xor32(uint32_t v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (__lane_id() & 32) ? p[0] : p[1];
+}
+__device__ __forceinline__ float lane_xor16(float v) { return __uint_as_float(lane_xor16(__float_as_uint(v))); }
+__device__ __forceinline__ float lane_xor32(float v) { return __uint_as_float(lane_xor32(__float_as_uint(v))); }
+__device__ __forceinline__ int lane_xor16(int v) { return (int)lane_xor16((uint32_t)v); }
+__device__ __forceinline__ int lane_xor32(int v) { return (int)lane_xor32((uint32_t)v); }
+
 // First-maximum argmax of (|v|, position) over aligned groups of GL lanes; every lane of a
 // group ends with the group's winner.  Butterfly steps: four DPP exchanges inside rows of 16
-// lanes, then lane-xor 16 and 32 through the LDS crossbar.
+// lanes, then lane-xor 16 and 32 by permlane swaps.
 template <int GL>
 __device__ __forceinline__ void group_argmax(float& babs, float& bv, int& bi) {
   argmax_dpp_step<kDppQuad1032>(babs, bv, bi);
@@ -74,9 +90,9 @@ __device__ __forceinline__ void group_argmax(float& babs, float& bv, int& bi) {
   argmax_dpp_step<kDppRowHalfMirror>(babs, bv, bi);
   argmax_dpp_step<kDppRowMirror>(babs, bv, bi);
   if constexpr (GL >= 32)
-    argmax_take(babs, bv, bi, __shfl_xor(babs, 16), __shfl_xor(bv, 16), __shfl_xor(bi, 16));
+    argmax_take(babs, bv, bi, lane_xor16(babs), lane_xor16(bv), lane_xor16(bi));
   if constexpr (GL >= 64)
-    argmax_take(babs, bv, bi, __shfl_xor(babs, 32), __shfl_xor(bv, 32), __shfl_xor(bi, 32));
+    argmax_take(babs, bv, bi, lane_xor32(babs), lane_xor32(bv), lane_xor32(bi));
 }
 
 // Sum over aligned groups of GL lanes, the same value in every lane of the group.
@@ -86,8 +102,8 @@ __device__ __forceinline__ float group_sum(float v) {
   v += dpp_f<kDppQuad2301>(v);
   v += dpp_f<kDppRowHalfMirror>(v);
   v += dpp_f<kDppRowMirror>(v);
-  if constexpr (GL >= 32) v += __shfl_xor(v, 16);
-  if constexpr (GL >= 64) v += __shfl_xor(v, 32);
+  if constexpr (GL >= 32) v += lane_xor16(v);
+  if constexpr (GL >= 64) v += lane_xor32(v);
   return v;
 }
 
@@ -97,8 +113,8 @@ __device__ __forceinline__ int group_min(int v) {
   v = min(v, dpp_i<kDppQuad2301>(v));
   v = min(v, dpp_i<kDppRowHalfMirror>(v));
   v = min(v, dpp_i<kDppRowMirror>(v));
-  if constexpr (GL >= 32) v = min(v, __shfl_xor(v, 16));
-  if constexpr (GL >= 64) v = min(v, __shfl_xor(v, 32));
+  if constexpr (GL >= 32) v = min(v, lane_xor16(v));
+  if constexpr (GL >= 64) v = min(v, lane_xor32(v));
   return v;
 }
 
