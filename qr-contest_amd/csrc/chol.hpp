@@ -11,9 +11,9 @@
 //   * the trailing update G_>,> -= R_k,>^T R_k,> (upper 64x64 tiles, MFMA) is split: the
 //     first diagonal tile -- the next diagonal block -- is updated into LDS by quadrants on
 //     waves 0, 1 and 3 (three SIMDs; its lower-left quadrant is never read), then, after a
-//     workgroup barrier, wave 0 factors it (one symmetric row per lane in registers, the scaled pivot row broadcast
-//     through LDS inside the wave, no barriers) and forms its inverse blocked by 32, while
-//     waves 1..7 update the other tiles.  The sequential diagonal work thus runs under the
+//     workgroup barrier, wave 0 factors it (rank-1 updates on MFMA with the block held in
+//     accumulators, no barriers) and forms its inverse blocked by 32, while waves 1..7 update
+//     the other tiles.  The sequential diagonal work thus runs under the
 //     trailing update.
 // The diagonal-block inverses go to Dinv ([n][64] per matrix) for the triangular solve that
 // follows.  info records the first column whose pivot was not positive (1-based; NaN
@@ -40,7 +40,7 @@ constexpr int kCholNb = 64;
 
 inline size_t chol_lds_bytes(int n, bool strip) {
   const size_t w = n > kCholNb ? (size_t)(n - kCholNb) : 1;
-  return sizeof(float) * (64 * 65 + 64 * 68 + 64 + 128 + 32 + (strip ? 64 * w + 64 : 0));
+  return sizeof(float) * (64 * 65 + 64 * 68 + 64 + 32 + (strip ? 64 * w + 64 : 0));
 }
 
 // Wave 0: factor the 64x64 diagonal block held in D (symmetric; the upper part is read) in
@@ -57,10 +57,9 @@ inline size_t chol_lds_bytes(int n, bool strip) {
 //   * u (the row past j) is the A and B operand of the 2-block product for (0,0) and (1,1), and
 //     with its halves swapped the B operand of the 32x32x2 product for (0,1).
 // So a step is a chain of MFMA -> readlane -> sqrt / rcp -> swap -> MFMA with no LDS round trip
-// and no per-lane loop over the row; rows of R go to LDS as they finish.  SB is unused here.
+// and no per-lane loop over the row; rows of R go to LDS as they finish.
 // The pivot's square root and reciprocal are the hardware's (1 ulp).
-__device__ __forceinline__ int chol_diag_wave(float* D, float* RT, float* RI, float* SB, int lane) {
-  (void)SB;
+__device__ __forceinline__ int chol_diag_wave(float* D, float* RT, float* RI, int lane) {
   asm volatile("" : "+v"(lane));  // lane-derived values stay here, not hoisted out of the caller's loop
   f32x32 dg;  // (0,0) in registers 0..15, (1,1) in 16..31
   f32x16 od;  // (0,1)
@@ -174,8 +173,7 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_c
   float* XT = D + 64 * 65;         // [64][65] (R_kk^-1)^T: XT[i][k] = Dinv_kk[k][i] ...
   float* RT = XT;                  // ... over [64][68] R_kk column-major while it is factored
   float* RI = XT + 64 * 68;        // [64] 1 / R[j][j] of the diagonal block
-  float* SB = RI + 64;             // [2][64] scaled pivot row broadcasts (wave 0)
-  float* red = SB + 128;           // [16]
+  float* red = RI + 64;            // [16]
   int* ffail = reinterpret_cast<int*>(red + 16);
   float* S = red + 32;             // block row [64][n-64] when strip_lds
 
@@ -345,7 +343,7 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(2))) void k_c
       }
       auto diag_factor = [&]() {
         wave_lds_order();
-        const int fail = chol_diag_wave(D, RT, RI, SB, lane);
+        const int fail = chol_diag_wave(D, RT, RI, lane);
         if (lane == 0 && fail != INT_MAX && fail < kbn && *ffail == INT_MAX) *ffail = k1 + fail + 1;
         wave_lds_order();
         chol_inverse_wave(RT, RI, D, XT, lane);
@@ -476,12 +474,12 @@ __global__ __launch_bounds__(kCholThreads) void k_chol_jitter(CholSplitArgs a) {
 // Wave 0 of a split-form launch: factor and invert the diagonal block at k0 held in D (upper
 // part; the identity past n), write R_kk (upper) and Dinv_kk, record a failed pivot in info.
 __device__ __forceinline__ void chol_split_factor(const CholSplitArgs& a, int b, int k0, float* D, float* XT,
-                                                  float* RI, float* SB, int lane) {
+                                                  float* RI, int lane) {
   const int n = a.n, kb = min(kCholNb, n - k0);
   float* G = a.G + b * a.sg;
   float* Dv = a.Dinv + (int64_t)b * n * 64;
   wave_lds_order();
-  const int fail = chol_diag_wave(D, XT, RI, SB, lane);
+  const int fail = chol_diag_wave(D, XT, RI, lane);
   if (lane == 0 && fail != INT_MAX && fail < kb && a.info[b] == 0) a.info[b] = k0 + fail + 1;
   wave_lds_order();
   chol_inverse_wave(XT, RI, D, XT, lane);
@@ -498,7 +496,6 @@ __global__ __launch_bounds__(64) void k_chol_diag(CholSplitArgs a) {
   __shared__ float D[64 * 65];
   __shared__ __attribute__((aligned(16))) float XT[64 * 68];  // RT while factoring, then XT
   __shared__ float RI[64];
-  __shared__ __attribute__((aligned(16))) float SB[128];
   const int n = a.n, k0 = a.k0, b = blockIdx.x, lane = threadIdx.x;
   const int kb = min(kCholNb, n - k0);
   const float* G = a.G + b * a.sg;
@@ -512,7 +509,7 @@ __global__ __launch_bounds__(64) void k_chol_diag(CholSplitArgs a) {
 #pragma unroll
     for (int i = 0; i < 64; ++i) D[i * 65 + lane] = (i < kb && lane < kb) ? v[i] : (i == lane ? 1.f : 0.f);
   }
-  chol_split_factor(a, b, k0, D, XT, RI, SB, lane);
+  chol_split_factor(a, b, k0, D, XT, RI, lane);
 }
 
 // R_k,> = Dinv_kk^T G_k,>: wave w of workgroup g takes the 32 columns starting at
@@ -617,7 +614,6 @@ __global__ __launch_bounds__(kCholSplitThreads) void k_chol_step(CholSplitArgs a
   __shared__ float D[64 * 65];
   __shared__ __attribute__((aligned(16))) float XT[64 * 68];  // RT while factoring, then XT
   __shared__ float RI[64];
-  __shared__ __attribute__((aligned(16))) float SB[128];
   const int n = a.n, k0 = a.k0, k1 = k0 + kCholNb, w = n - k1;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t pid = blockIdx.x;
@@ -650,7 +646,7 @@ __global__ __launch_bounds__(kCholSplitThreads) void k_chol_step(CholSplitArgs a
       }
     }
     __syncthreads();
-    if (wid == 0) chol_split_factor(a, b, k1, D, XT, RI, SB, lane);
+    if (wid == 0) chol_split_factor(a, b, k1, D, XT, RI, lane);
     return;
   }
   const int64_t q = pid - a.nb, b = q / a.njob;
