@@ -481,6 +481,52 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_small(SmallArgs a) {
 
   // ---- chart: sign-ruled unpivoted elimination of the Q rows
   float my_s = 1.f;
+  if constexpr (G == 2) {
+    // two matrices per wave, no pivoting: each Q is held twice in v_mfma_f32_32x32x1_2b_f32
+    // accumulators, as itself (D1[i][c] = x[i][c]) and transposed (D2[c][i] = x[i][c]), block g
+    // for matrix g.  Step k reads its pivot row from D1 and its column (the multipliers' source)
+    // from D2 -- each one register of one half-wave, gathered into lane order by a permlane32
+    // swap -- and the rank-1 update x -= mult pivot_row^T is one 2-block MFMA per copy.  The
+    // multipliers (the reflector tails Y) go to As as they are formed.
+    lds_store_row<NP>(myA + r * LD, x);
+    wave_lds_order();
+    f32x32 d1, d2;
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+      const int i = acc_row(q & 15, lane), c = lane & 31;
+      d1[q] = As[(q >> 4) * MAT + i * LD + c];
+      d2[q] = As[(q >> 4) * MAT + c * LD + i];
+    }
+    wave_lds_order();  // the Y stores below stay behind these reads
+    static_for<0, NP>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      constexpr int HK = (k / 4) % 2, RK = 4 * (k / 8) + k % 4;
+      if (k < n) {
+        int rr = r;
+        asm volatile("" : "+v"(rr));  // the step's lane masks are formed here, not hoisted
+        const float e0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(d1[RK]), k + 32 * HK));
+        const float e1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(d1[16 + RK]), k + 32 * HK));
+        const float d = gup ? e1 : e0;
+        const float pp = 1.f - d, pm = 1.f + d;
+        const bool plus = fabsf(pp) >= fabsf(pm);  // |1-d| >= |1+d|, the tie d = 0 takes +1
+        const float sk = plus ? 1.f : -1.f;
+        const float piv = plus ? pp : pm;
+        if (rr == k) my_s = sk;
+        const float2 pr = lane_halves(d1[RK], d1[16 + RK]);  // lane c: x[k][c]
+        const float2 pc = lane_halves(d2[RK], d2[16 + RK]);  // lane i: x[i][k]
+        const float prow = HK == 0 ? pr.x : pr.y, pcol = HK == 0 ? pc.x : pc.y;
+        const float mult = (rr > k && rr < n) ? (-sk * pcol) / piv : 0.f;
+        if (rr > k) myA[rr * LD + k] = mult;  // Y[i][k]
+        if (k + 1 < n) {
+          const float u = (rr > k) ? prow : 0.f;
+          d1 = mfma_2b(-mult, u, d1);
+          d2 = mfma_2b(-u, mult, d2);
+        }
+      }
+    });
+    wave_lds_order();
+    lds_load_row<NP>(x, myA + r * LD);  // row r of Y (below the diagonal) for the packing below
+  } else {
   static_for<0, NP>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
     if (k < n) {
@@ -514,6 +560,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_small(SmallArgs a) {
 
   // ---- tau_k = 2 / (1 + sum_{i>k} Y[i][k]^2): Y rows -> As, lane k sums column k
   lds_store_row<NP>(myA + r * LD, x);
+  }
   wave_lds_order();
   if (live && mat < a.batch) {
     float ss = 0.f;
