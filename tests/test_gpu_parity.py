@@ -282,12 +282,16 @@ def test_dtype_shape_and_stride_contract(rnr):
     assert torch.equal(A0, A1)
 
 
-def test_nonfinite_input_follows_the_reference(rnr):
+@pytest.mark.parametrize("n", [32, 100, 300, 640])
+def test_nonfinite_input_follows_the_reference(rnr, n):
     """NaN reaches the Gram and the Cholesky raises (reference :76); an Inf is absorbed by the
     LU's 1/Inf pivot scaling, so the reference returns a non-finite R for that matrix and no
-    error -- the oracle does both on the same input, and so must the HIP path."""
+    error -- the oracle does both on the same input, and so must the HIP path: the one-launch
+    kernel (n = 32), the per-block Cholesky (100), the fused kernels (300) and the split form
+    (640 with three matrices)."""
+    print(f"[case] nonfinite n={n}", flush=True)
     g = torch.Generator().manual_seed(0)
-    A = torch.randn(3, 32, 32, generator=g)
+    A = torch.randn(3, n, n, generator=g)
     A[1, 5, 7] = float("nan")
     with pytest.raises(RuntimeError, match="positive-definite"):
         orc.custom_kernel(A)
