@@ -196,6 +196,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   };
 
   const int klo = a.klo_from_j ? j0 : 0;
+  // the unit-lower L is zero above its diagonal: this wave's operand columns start at i0 + wi0
+  // and j0 + wj0, so its chunks below both multiply zeros only and their MFMAs are skipped
+  // (the chunk is still staged: the other waves of the tile read it)
+  const int kz = a.klo_from_j ? max(i0 + wi0, j0 + wj0) : 0;
   int buf = 0;
   gload(klo);
   lstore(0, klo);
@@ -205,7 +209,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     for (int kc = klo; kc < n; kc += BK) {
       const bool more = kc + BK < n;
       if (more) gload(kc + BK);
-      if constexpr (LOW != 2) {
+      if (LOW != 2 && kc + BK > kz) {
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
           const int k = kk + h;
