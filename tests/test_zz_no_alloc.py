@@ -43,9 +43,10 @@ def _no_alloc(native, A, H, tau, info):
 
 def test_noalloc_equals_the_workspace_entry_point_twice(mods):
     native, wl = mods
-    # (batch, n): the blocked path at the headline size, then a smaller blocked problem, then
-    # the fused small-n path (no scratch at all)
-    for b, n, seed in ((24, 512, 21), (5, 200, 22), (40, 48, 23)):
+    # (batch, n), each needing less scratch than the one before: the blocked path at the
+    # headline size, the split form (small batch at n > 512), a smaller blocked problem, the
+    # per-block Cholesky at n <= 128, then the fused small-n path (no scratch at all)
+    for b, n, seed in ((24, 512, 21), (2, 640, 24), (5, 200, 22), (6, 100, 25), (40, 48, 23)):
         print(f"[case] noalloc b={b} n={n}", flush=True)
         A = wl.make_batch(4, batch=b, n=n, seed=seed).to(DEV)
         H0, t0, i0 = _with_workspace(native, A)
