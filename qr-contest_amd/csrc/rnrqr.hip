@@ -132,8 +132,12 @@ void launch_lu_trail_g(const LuArgs& a, int S, int kg, int cb, int ce, int64_t b
   // rows per workgroup: each workgroup forms its chunk's U itself, so it takes as many rows as
   // still leaves about one workgroup per two CUs (at least 256; measured at 16 x 2048 against
   // thresholds of 2 to 8 workgroups per CU, which redo the U more often: 20.0 -> 19.5 ms)
-  int rpw = kLuTrailRows;
-  while (rpw < rows && batch * nchunk * ((rows + 2 * rpw - 1) / (2 * rpw)) >= 128) rpw *= 2;
+  // The catch-up launches (S < 4: one 32-column chunk, a U of a few 32 x 32 blocks that costs
+  // little to redo) take 128 rows, one row tile per wave, for more workgroups (16 x 2048:
+  // 19.1 -> 18.7 ms against 256 rows and more).
+  int rpw = S < 4 ? 128 : kLuTrailRows;
+  if (S == 4)
+    while (rpw < rows && batch * nchunk * ((rows + 2 * rpw - 1) / (2 * rpw)) >= 128) rpw *= 2;
   const int nrg = (rows + rpw - 1) / rpw;
   const dim3 grid((unsigned)(batch * nchunk * nrg)), block(kLuTrailThreads);
   const int64_t xslot = batch * 1024;
