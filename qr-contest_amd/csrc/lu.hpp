@@ -51,12 +51,18 @@ constexpr int kLuThreads = 512;
 // workgroups per CU instead of three (1024 x 128: LU 0.246 -> 0.168 ms, chart 0.167 -> 0.134).
 inline int lu_panel_nb(int n) { return n <= 128 ? 32 : (n <= 512 ? 64 : (n <= 1024 ? 32 : 16)); }
 
+// direct (split) panels: 1024-thread workgroups, each wave with a row-staging area of 32 rows
+constexpr int kLuDirectWaves = 16;
+constexpr int kLuStageLd = 36;  // staging row stride (floats): 16 lanes' rows cover the 64 banks
+constexpr int kLuStageFloats = 32 * kLuStageLd + 32;  // per wave: 32 rows + their target rows (int)
+
 // panel [n][nb+1] | -U12 chunk [nb][64] | row map [n] | pivot keys [3] (u64) | pivot row
-// slots [2][nb+4]
+// slots [2][nb+4] | (direct) row staging [waves][kLuStageFloats]
 inline size_t lu_lds_bytes(int n, int nb, bool direct = false) {
   const size_t p = ((size_t)(direct ? nb : n) * (nb + 1) + 3) & ~(size_t)3;
   const size_t pl = ((size_t)n + 3) & ~(size_t)3;
-  return sizeof(float) * (p + (size_t)nb * 64 + pl + 8 + 2 * (size_t)(nb + 4));
+  const size_t stage = direct ? (size_t)kLuDirectWaves * kLuStageFloats : 0;
+  return sizeof(float) * (p + (size_t)nb * 64 + pl + 8 + 2 * (size_t)(nb + 4) + stage);
 }
 
 // SPLIT = true: one launch factors only panel a.k0 and stops before its trailing update,
@@ -139,6 +145,11 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(T > 512 ? 4 :
   unsigned long long* pkeys =                       // [3] pivot keys (LU), by step mod 3
       reinterpret_cast<unsigned long long*>(reinterpret_cast<float*>(pl) + ((n + 3) & ~3));
   float* slots = reinterpret_cast<float*>(pkeys) + 8;  // [2][NB+4] pivot rows, by column parity
+  // DIRECT: this wave's row staging (32 rows at stride kLuStageLd, then their target rows), so the
+  // panel's rows move between HBM and the threads' registers row-contiguously (8 lanes a row)
+  // instead of one row per lane (64 rows, 16 bytes each, per memory instruction)
+  static_assert(!DIRECT || T / 64 == kLuDirectWaves, "direct panels: staging sized for 16 waves");
+  float* const stg = slots + 2 * (NB + 4);
 
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5, l16 = lane & 15, q4 = lane >> 4;
@@ -197,25 +208,42 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(T > 512 ? 4 :
     __syncthreads();
     float row[RPT][NB];
     if constexpr (DIRECT) {
+      // per half-wave: its 32 rows loaded row-contiguously into the staging (lane: row
+      // it * 8 + lane / 8, float4 lane % 8), then each thread takes its own row from there
+      static_assert(NB == 32, "direct panels are 32 wide");
+      float* wst = stg + wid * kLuStageFloats;
 #pragma unroll
-      for (int q = 0; q < RPT; ++q) {
-        const int r = tid + T * q;
-        const int pr = (r < m) ? (PIVOT ? pl[k0 + r] : k0 + r) : 0;
-        const float* srow = cur + (int64_t)pr * n + k0;
-        if (a.vec4 && kb == NB) {
+      for (int q = 0; q < RPT; ++q)
 #pragma unroll
-          for (int c4 = 0; c4 < NB4; ++c4) {
-            const float4 v = *reinterpret_cast<const float4*>(srow + 4 * c4);
-            row[q][4 * c4] = (r < m) ? v.x : 0.f;
-            row[q][4 * c4 + 1] = (r < m) ? v.y : 0.f;
-            row[q][4 * c4 + 2] = (r < m) ? v.z : 0.f;
-            row[q][4 * c4 + 3] = (r < m) ? v.w : 0.f;
+        for (int h2 = 0; h2 < 2; ++h2) {
+#pragma unroll
+          for (int it = 0; it < 4; ++it) {
+            const int sr = it * 8 + (lane >> 3), c4 = lane & 7;
+            const int r = wid * 64 + h2 * 32 + sr + T * q;
+            const int pr = (r < m) ? (PIVOT ? pl[k0 + r] : k0 + r) : 0;
+            const float* src4 = cur + (int64_t)pr * n + k0 + 4 * c4;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (a.vec4) {
+              if (r < m && 4 * c4 < kb) v = *reinterpret_cast<const float4*>(src4);
+            } else if (r < m) {
+              v.x = (4 * c4 < kb) ? src4[0] : 0.f;
+              v.y = (4 * c4 + 1 < kb) ? src4[1] : 0.f;
+              v.z = (4 * c4 + 2 < kb) ? src4[2] : 0.f;
+              v.w = (4 * c4 + 3 < kb) ? src4[3] : 0.f;
+            }
+            *reinterpret_cast<float4*>(wst + sr * kLuStageLd + 4 * c4) = v;
           }
-        } else {
+          wave_lds_order();
+          if ((lane >> 5) == h2) {
+            const int sr = lane & 31;
 #pragma unroll
-          for (int c = 0; c < NB; ++c) row[q][c] = (r < m && c < kb) ? srow[c] : 0.f;
+            for (int c4 = 0; c4 < NB4; ++c4) {
+              const float4 v = *reinterpret_cast<const float4*>(wst + sr * kLuStageLd + 4 * c4);
+              row[q][4 * c4] = v.x; row[q][4 * c4 + 1] = v.y; row[q][4 * c4 + 2] = v.z; row[q][4 * c4 + 3] = v.w;
+            }
+          }
+          wave_lds_order();  // the next half's staging stores stay behind these reads
         }
-      }
     } else {
 #pragma unroll
       for (int q = 0; q < RPT; ++q) {
@@ -389,21 +417,46 @@ __global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(T > 512 ? 4 :
 #pragma unroll
           for (int c = 0; c < NB; ++c) P[sw(pos[q], c)] = row[q][c];
         }
-        if constexpr (DIRECT) {
-          float* drow = dst + (int64_t)(PIVOT ? phys[q] : k0 + r) * n + k0;
-          if (a.vec4 && kb == NB) {
-#pragma unroll
-            for (int c4 = 0; c4 < NB4; ++c4)
-              *reinterpret_cast<float4*>(drow + 4 * c4) =
-                  make_float4(row[q][4 * c4], row[q][4 * c4 + 1], row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
-          } else {
-#pragma unroll
-            for (int c = 0; c < NB; ++c)
-              if (c < kb) drow[c] = row[q][c];
-          }
-        }
         if (PIVOT) pl[k0 + pos[q]] = phys[q];
       }
+    }
+    if constexpr (DIRECT) {
+      // every row straight back to its row of HBM, through the staging: per half-wave, the
+      // threads' rows and target rows in, then 8 lanes a row out
+      float* wst = stg + wid * kLuStageFloats;
+      int* wdst = reinterpret_cast<int*>(wst + 32 * kLuStageLd);
+#pragma unroll
+      for (int q = 0; q < RPT; ++q)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          if ((lane >> 5) == h2) {
+            const int sr = lane & 31, r = tid + T * q;
+#pragma unroll
+            for (int c4 = 0; c4 < NB4; ++c4)
+              *reinterpret_cast<float4*>(wst + sr * kLuStageLd + 4 * c4) =
+                  make_float4(row[q][4 * c4], row[q][4 * c4 + 1], row[q][4 * c4 + 2], row[q][4 * c4 + 3]);
+            wdst[sr] = (r < m) ? (PIVOT ? phys[q] : k0 + r) : -1;
+          }
+          wave_lds_order();
+#pragma unroll
+          for (int it = 0; it < 4; ++it) {
+            const int sr = it * 8 + (lane >> 3), c4 = lane & 7;
+            const int dr = wdst[sr];
+            const float4 v = *reinterpret_cast<const float4*>(wst + sr * kLuStageLd + 4 * c4);
+            float* d4 = dst + (int64_t)max(dr, 0) * n + k0 + 4 * c4;
+            if (dr >= 0) {
+              if (a.vec4) {
+                if (4 * c4 < kb) *reinterpret_cast<float4*>(d4) = v;
+              } else {
+                if (4 * c4 < kb) d4[0] = v.x;
+                if (4 * c4 + 1 < kb) d4[1] = v.y;
+                if (4 * c4 + 2 < kb) d4[2] = v.z;
+                if (4 * c4 + 3 < kb) d4[3] = v.w;
+              }
+            }
+          }
+          wave_lds_order();  // the next half's staging stores stay behind these reads
+        }
     }
     if (!PIVOT && tid < kb) a.s[(int64_t)b * n + k0 + tid] = my_s;
     __syncthreads();
